@@ -1,0 +1,132 @@
+/*
+ * C-ABI of the MI355X (gfx950) UVU tensor-product convolution library.
+ *
+ * The reference binds one pybind11 module per irreps configuration, generated
+ * and compiled at prepare time:
+ *   - run_uvu_conv_fwd_ordered(x, y, weight, env?, l0?, src, rowptr,
+ *       node_order, node_tiers?, out, num_nodes)
+ *       (src/lunatp/uvu_conv/kernels/forward.py:1117-1128)
+ *   - run_uvu_conv_bwd(x, y, w, go, dst, edge_ids, seg_*..., gx_partial,
+ *       gy_partial, gx, gy, gw, nodes, edges, segments, env?, ge_partial?, ge?,
+ *       grad_l0?)  (src/lunatp/uvu_conv/kernels/backward.py:505-512)
+ *   - the double-backward launcher (double_backward.py:1635-...)
+ * Here one shared library holds the launchers; a plan object holds the
+ * per-configuration kernels, which the library emits as HIP source from the
+ * path specification and compiles for gfx950 with hipRTC (code objects are
+ * cached on disk).  Every device buffer is allocated by the caller; the
+ * library never allocates device memory.  Launches are ordered on the
+ * caller's stream.  Every function returns 0 on success or a non-zero error
+ * code; luna_last_error() gives the message of the last failure on the
+ * calling thread.
+ *
+ * Data layout (row-major, contiguous, dtype of the plan):
+ *   x   [N, in1_dim]      node features, e3nn layout (copy-major irreps)
+ *   y   [E, in2_dim]      edge attributes
+ *   w   [E, weight_numel] per-edge path weights, w[e, w_off + u*w_stride + v]
+ *   env [E] or NULL       per-edge envelope multiplying each message
+ *   out [N, out_dim]
+ *   l0  [E, l0_dim]       optional scalar-path features (before env)
+ * Graph tables are int32: src[E], dst[E] (dst sorted ascending),
+ * dst_rowptr[N+1], src_rowptr[N+1], edge_ids_by_src[E], node_order[N],
+ * source_node_order[N].
+ */
+#ifndef LUNAEQ_AMD_H
+#define LUNAEQ_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct LunaUvuPlan LunaUvuPlan;
+
+/* Opaque stream handle: a hipStream_t (NULL = the null stream). */
+typedef void* LunaStream;
+
+/* Static facts about a plan, filled by luna_uvu_plan_info. */
+typedef struct LunaUvuPlanInfo {
+  int32_t dtype_bits;        /* 32 or 64 */
+  int32_t in1_dim, in2_dim, out_dim, weight_numel, l0_dim;
+  int32_t num_paths;
+  int32_t fwd_needs_zero;    /* out must be zero-filled before luna_uvu_conv_fwd */
+  int32_t bwd_gx_needs_zero; /* gx must be zero-filled before luna_uvu_conv_bwd */
+  int32_t num_fwd_launches;  /* launches per forward call */
+  int32_t gy_parts;          /* partial slots of the edge-attribute gradient */
+} LunaUvuPlanInfo;
+
+/* Text of the last error on this thread ("" if none). */
+const char* luna_last_error(void);
+
+/* Library version string. */
+const char* luna_version(void);
+
+/* Number of visible HIP devices (0 without a GPU); never fails. */
+int luna_device_count(void);
+
+/*
+ * Build a plan from a path specification (the metadata the reference builds in
+ * build_uvu_conv_metadata, src/lunatp/uvu_conv/kernels/utils.py:23-119):
+ *
+ *   "LUNAUVU1 <dtype_bits> <in1> <in2> <out> <weight_numel> <npaths> <l0_dim>"
+ *   then per path:
+ *   "<x_off> <y_off> <out_off> <w_off> <w_stride> <channels> <d1> <d2> <d3>
+ *    <l0_col or -1> <nterms> (<i> <j> <k> <coefficient>)*nterms"
+ *
+ * Coefficients already include the path weight.  Kernels are emitted and
+ * compiled here (or loaded from the code-object cache in cache_dir, which may
+ * be NULL for no cache); loading onto a device is deferred to first launch.
+ * replaces: LunaTPUVUConv / configure_uvu_conv / load_forward
+ * (src/lunatp/interface.py:353-367, uvu_conv/kernels/utils.py:121-158,
+ * uvu_conv/kernels/forward.py:1249-1288).
+ */
+int luna_uvu_plan_create(const char* spec, const char* cache_dir, LunaUvuPlan** plan);
+int luna_uvu_plan_destroy(LunaUvuPlan* plan);
+int luna_uvu_plan_info(const LunaUvuPlan* plan, LunaUvuPlanInfo* info);
+
+/*
+ * Compile (or fetch from cache) every kernel variant a plan can launch, without
+ * touching a device.  Used to warm the code-object cache ahead of time.
+ */
+int luna_uvu_plan_precompile(LunaUvuPlan* plan);
+
+/*
+ * Forward: out[t] = sum over edges e with dst[e]==t of env[e] * TP(x[src[e]], y[e], w[e]).
+ * l0 may be NULL; when given, l0[e, :] receives the per-edge scalar-path
+ * contributions before env.
+ * replaces: run_uvu_conv_fwd_ordered (src/lunatp/uvu_conv/kernels/forward.py:1117-1128)
+ */
+int luna_uvu_conv_fwd(const LunaUvuPlan* plan,
+                      const void* x, const void* y, const void* w, const void* env,
+                      const int32_t* src, const int32_t* dst_rowptr,
+                      const int32_t* node_order,
+                      void* out, void* l0,
+                      int64_t num_nodes, int64_t num_edges, LunaStream stream);
+
+/* Bytes of device workspace luna_uvu_conv_bwd needs for this problem size. */
+int luna_uvu_conv_bwd_workspace(const LunaUvuPlan* plan, int64_t num_nodes,
+                                int64_t num_edges, size_t* bytes);
+
+/*
+ * First-order backward.  g = dL/dout [N, out_dim]; gl0 = dL/dl0 [E, l0_dim] or
+ * NULL.  Writes gx [N, in1], gy [E, in2], gw [E, weight_numel] and, when env
+ * is given and genv is not NULL, genv [E].  Any of gx/gy/gw may be NULL to skip
+ * it.  workspace must hold luna_uvu_conv_bwd_workspace bytes.
+ * replaces: run_uvu_conv_bwd (src/lunatp/uvu_conv/kernels/backward.py:505-512)
+ */
+int luna_uvu_conv_bwd(const LunaUvuPlan* plan,
+                      const void* x, const void* y, const void* w, const void* env,
+                      const void* g, const void* gl0,
+                      const int32_t* dst, const int32_t* src_rowptr,
+                      const int32_t* edge_ids_by_src,
+                      const int32_t* source_node_order,
+                      void* gx, void* gy, void* gw, void* genv,
+                      void* workspace, size_t workspace_bytes,
+                      int64_t num_nodes, int64_t num_edges, LunaStream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LUNAEQ_AMD_H */

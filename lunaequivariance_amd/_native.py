@@ -1,0 +1,82 @@
+"""Loader and thin ctypes binding of the C-ABI library ``liblunaeq_amd.so``.
+
+The library is built in-tree by ``lunaequivariance_amd.build.build_library``;
+importing this module never compiles anything.  A missing library raises
+``RuntimeError`` at first use: there is no CPU fallback for the kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+LIBRARY_PATH = PACKAGE_DIR / "liblunaeq_amd.so"
+DEFAULT_CACHE_DIR = PACKAGE_DIR / "_kcache"
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "dtype_bits", "in1_dim", "in2_dim", "out_dim", "weight_numel", "l0_dim",
+        "num_paths", "fwd_needs_zero", "bwd_gx_needs_zero", "num_fwd_launches", "gy_parts",
+    )]
+
+
+# Exported symbols and their prototypes: (restype, argtypes).
+_VP, _I64, _I32P = ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p
+PROTOTYPES = {
+    "luna_last_error": (ctypes.c_char_p, []),
+    "luna_version": (ctypes.c_char_p, []),
+    "luna_device_count": (ctypes.c_int, []),
+    "luna_uvu_plan_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_VP)]),
+    "luna_uvu_plan_destroy": (ctypes.c_int, [_VP]),
+    "luna_uvu_plan_info": (ctypes.c_int, [_VP, ctypes.POINTER(PlanInfo)]),
+    "luna_uvu_plan_precompile": (ctypes.c_int, [_VP]),
+    "luna_uvu_conv_fwd": (ctypes.c_int, [_VP] + [_VP] * 4 + [_I32P] * 3 + [_VP, _VP, _I64, _I64, _VP]),
+    "luna_uvu_conv_bwd_workspace": (ctypes.c_int, [_VP, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
+    "luna_uvu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 4 + [_VP] * 5
+                          + [ctypes.c_size_t, _I64, _I64, _VP]),
+}
+
+_lib = None
+
+
+def library_available() -> bool:
+    return LIBRARY_PATH.exists()
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C-ABI library (raises RuntimeError if it was never built)."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY_PATH.exists():
+            raise RuntimeError(
+                f"{LIBRARY_PATH} is missing: build it with "
+                "`python -c 'import lunaequivariance_amd.build as b; b.build_library()'`")
+        handle = ctypes.CDLL(str(LIBRARY_PATH))
+        for name, (restype, argtypes) in PROTOTYPES.items():
+            function = getattr(handle, name)
+            function.restype = restype
+            function.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        message = lib().luna_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {message}")
+
+
+def cache_dir() -> str:
+    return os.environ.get("LUNAEQ_AMD_CACHE", str(DEFAULT_CACHE_DIR))
+
+
+def ptr(tensor) -> int | None:
+    """Device address of a tensor, or None for an absent optional tensor."""
+    return None if tensor is None else tensor.data_ptr()
+
+
+__all__ = ["lib", "check", "cache_dir", "ptr", "PlanInfo", "PROTOTYPES", "LIBRARY_PATH",
+           "library_available"]

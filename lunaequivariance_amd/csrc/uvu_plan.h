@@ -1,0 +1,86 @@
+// Internal declarations shared by the UVU convolution planner, emitter and
+// runtime.  Not part of the public C-ABI (include/lunaeq_amd.h is).
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+namespace luna {
+
+// One sparse Clebsch-Gordan entry, already scaled by the path weight.
+struct Term {
+  int i, j, k;
+  double c;
+};
+
+// One lowered UVU path: input block x_off (channels x d1), edge block y_off
+// (d2 components), output block out_off (channels x d3), weights
+// w[e, w_off + u * w_stride].
+struct Path {
+  int x_off, y_off, out_off, w_off, w_stride, channels, d1, d2, d3, l0_col;
+  std::vector<Term> terms;
+};
+
+struct Spec {
+  int dtype_bits = 32;
+  int in1 = 0, in2 = 0, out = 0, wnum = 0, l0_dim = 0;
+  std::vector<Path> paths;
+};
+
+// An accumulator block: one output block (out_off, d3) of one group.
+struct AccBlock {
+  int out_off, d3;
+  bool accumulate;  // read-modify-write instead of plain store
+};
+
+// Paths sharing one input block (x_off, d1, channels), run by one wave per
+// (node, 64-channel chunk).
+struct Group {
+  int x_off, d1, channels, chunks;
+  std::vector<int> paths;            // indices into Spec::paths
+  std::vector<AccBlock> blocks;      // forward output blocks
+  std::vector<int> path_block;       // path -> index in blocks
+  int phase = 0;
+  int slot_base = 0;                 // first grid.y slot of this group in its phase
+  bool gx_accumulate = false;        // backward: gx block shared with another group
+  int gy_slot_base = 0;              // backward: first partial slot of this group
+};
+
+struct Plan {
+  Spec spec;
+  std::vector<Group> fwd_groups;     // forward groups, each with a phase
+  int fwd_phases = 0;
+  std::vector<int> phase_slots;      // grid.y per forward phase
+  bool fwd_needs_zero = false;
+  std::vector<Group> bwd_groups;     // backward groups (one launch)
+  int bwd_phases = 0;                // backward launches
+  std::vector<int> bwd_phase_slots;  // grid.y per backward launch
+  int gy_parts = 0;                  // partial slots for the gy reduction
+  bool bwd_gx_needs_zero = false;
+  std::string cache_dir;
+
+  // Compiled code objects per variant key, and loaded modules per device.
+  std::mutex lock;
+  std::map<std::string, std::vector<char>> code;
+  std::map<std::pair<std::string, int>, void*> modules;  // (variant, device) -> hipModule_t
+};
+
+Spec parse_spec(const std::string& text);
+void build_schedule(Plan& plan);
+
+// Emitted HIP source of one kernel module variant.
+std::string emit_forward(const Plan& plan, bool env, bool l0);
+std::string emit_backward(const Plan& plan, bool env, bool gl0);
+
+// Compile HIP source for gfx950 with hipRTC, through the on-disk cache.
+std::vector<char> compile_hip(const std::string& source, const std::string& cache_dir,
+                              const std::string& tag);
+
+[[noreturn]] void fail(const std::string& message);
+
+}  // namespace luna

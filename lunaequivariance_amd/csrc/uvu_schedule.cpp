@@ -1,0 +1,266 @@
+// Path specification parsing and launch scheduling for the UVU convolution.
+//
+// Paths that read the same input block (x_off, d1, channels) form a group, so
+// a wave gathers each source row's block once per edge and keeps every output
+// block of the group in registers.  Output blocks written by more than one
+// group are separated into phases (one launch each) and accumulated, which
+// reproduces the reference's summation of aliased outputs
+// (src/lunatp/uvu_conv/kernels/utils.py:135-152) without atomics.
+#include <algorithm>
+#include <map>
+#include <tuple>
+#include <cstdio>
+#include <cstdlib>
+#include <sstream>
+#include <stdexcept>
+
+#include "uvu_plan.h"
+
+namespace luna {
+
+namespace {
+
+constexpr int kWave = 64;
+// Upper bound on live output accumulators per lane for one group.
+constexpr int kMaxAccumulators = 64;
+
+int read_int(std::istringstream& in, const char* what) {
+  long long value;
+  if (!(in >> value)) fail(std::string("spec: expected integer for ") + what);
+  if (value < -1 || value > (1LL << 31) - 1) fail(std::string("spec: value out of range for ") + what);
+  return static_cast<int>(value);
+}
+
+double read_real(std::istringstream& in) {
+  std::string token;
+  if (!(in >> token)) fail("spec: expected coefficient");
+  char* end = nullptr;
+  double value = std::strtod(token.c_str(), &end);
+  if (end == token.c_str() || *end != '\0') fail("spec: bad coefficient '" + token + "'");
+  return value;
+}
+
+bool ranges_overlap(long a0, long a1, long b0, long b1) { return a0 < b1 && b0 < a1; }
+
+}  // namespace
+
+Spec parse_spec(const std::string& text) {
+  std::istringstream in(text);
+  std::string magic;
+  in >> magic;
+  if (magic != "LUNAUVU1") fail("spec: missing LUNAUVU1 header");
+  Spec s;
+  s.dtype_bits = read_int(in, "dtype");
+  if (s.dtype_bits != 32 && s.dtype_bits != 64) fail("spec: dtype must be 32 or 64");
+  s.in1 = read_int(in, "in1");
+  s.in2 = read_int(in, "in2");
+  s.out = read_int(in, "out");
+  s.wnum = read_int(in, "weight_numel");
+  int npaths = read_int(in, "npaths");
+  s.l0_dim = read_int(in, "l0_dim");
+  if (npaths <= 0) fail("spec: UVU convolution needs at least one path");
+  for (int p = 0; p < npaths; ++p) {
+    Path q;
+    q.x_off = read_int(in, "x_off");
+    q.y_off = read_int(in, "y_off");
+    q.out_off = read_int(in, "out_off");
+    q.w_off = read_int(in, "w_off");
+    q.w_stride = read_int(in, "w_stride");
+    q.channels = read_int(in, "channels");
+    q.d1 = read_int(in, "d1");
+    q.d2 = read_int(in, "d2");
+    q.d3 = read_int(in, "d3");
+    q.l0_col = read_int(in, "l0_col");
+    int nterms = read_int(in, "nterms");
+    if (q.channels <= 0) fail("spec: UVU convolution requires positive channels for every path");
+    if (q.d1 <= 0 || q.d2 <= 0 || q.d3 <= 0 || q.w_stride <= 0) fail("spec: bad path dimensions");
+    if ((long)q.x_off + (long)q.channels * q.d1 > s.in1 || q.x_off < 0)
+      fail("spec: input block outside in1_dim");
+    if (q.y_off < 0 || q.y_off + q.d2 > s.in2) fail("spec: edge block outside in2_dim");
+    if (q.out_off < 0 || (long)q.out_off + (long)q.channels * q.d3 > s.out)
+      fail("spec: output block outside out_dim");
+    if (q.w_off < 0 || (long)q.w_off + (long)(q.channels - 1) * q.w_stride >= s.wnum)
+      fail("spec: weight block outside weight_numel");
+    if (q.l0_col >= 0 && (q.d3 != 1 || q.l0_col + q.channels > s.l0_dim))
+      fail("spec: l0 column outside l0_dim");
+    for (int t = 0; t < nterms; ++t) {
+      Term term;
+      term.i = read_int(in, "i");
+      term.j = read_int(in, "j");
+      term.k = read_int(in, "k");
+      term.c = read_real(in);
+      if (term.i < 0 || term.i >= q.d1 || term.j < 0 || term.j >= q.d2 || term.k < 0 || term.k >= q.d3)
+        fail("spec: coefficient index outside the path's irreps");
+      q.terms.push_back(term);
+    }
+    s.paths.push_back(std::move(q));
+  }
+  return s;
+}
+
+namespace {
+
+// Split the paths sharing one input block into groups whose output blocks fit
+// the accumulator budget.  Paths writing the same output block stay together.
+std::vector<Group> make_groups(const Spec& spec) {
+  std::map<std::tuple<int, int, int>, std::vector<int>> by_input;
+  std::vector<std::tuple<int, int, int>> key_order;
+  for (int p = 0; p < (int)spec.paths.size(); ++p) {
+    const Path& q = spec.paths[p];
+    auto key = std::make_tuple(q.x_off, q.d1, q.channels);
+    if (!by_input.count(key)) key_order.push_back(key);
+    by_input[key].push_back(p);
+  }
+  std::vector<Group> groups;
+  for (const auto& key : key_order) {
+    const std::vector<int>& members = by_input[key];
+    // Output blocks of this input block, in first-use order.
+    std::vector<std::pair<int, int>> blocks;
+    std::map<std::pair<int, int>, std::vector<int>> block_paths;
+    for (int p : members) {
+      auto b = std::make_pair(spec.paths[p].out_off, spec.paths[p].d3);
+      if (!block_paths.count(b)) blocks.push_back(b);
+      block_paths[b].push_back(p);
+    }
+    // First-fit by decreasing width.
+    std::vector<std::pair<int, int>> sorted = blocks;
+    std::stable_sort(sorted.begin(), sorted.end(),
+                     [](const auto& a, const auto& b) { return a.second > b.second; });
+    std::vector<std::pair<int, std::vector<std::pair<int, int>>>> bins;
+    for (const auto& b : sorted) {
+      bool placed = false;
+      for (auto& bin : bins) {
+        if (bin.first + b.second <= kMaxAccumulators) {
+          bin.first += b.second;
+          bin.second.push_back(b);
+          placed = true;
+          break;
+        }
+      }
+      if (!placed) bins.push_back({b.second, {b}});
+    }
+    for (auto& bin : bins) {
+      Group g;
+      g.x_off = std::get<0>(key);
+      g.d1 = std::get<1>(key);
+      g.channels = std::get<2>(key);
+      g.chunks = (g.channels + kWave - 1) / kWave;
+      // Keep the original block order inside the bin.
+      for (const auto& b : blocks) {
+        if (std::find(bin.second.begin(), bin.second.end(), b) == bin.second.end()) continue;
+        int index = (int)g.blocks.size();
+        g.blocks.push_back({b.first, b.second, false});
+        for (int p : block_paths[b]) {
+          g.paths.push_back(p);
+          g.path_block.push_back(index);
+        }
+      }
+      groups.push_back(std::move(g));
+    }
+  }
+  return groups;
+}
+
+// Greedy phase assignment: groups in one phase touch disjoint ranges.
+template <typename RangesOf>
+int assign_phases(std::vector<Group>& groups, RangesOf ranges_of) {
+  std::vector<std::vector<std::pair<long, long>>> phase_ranges;
+  for (Group& g : groups) {
+    auto mine = ranges_of(g);
+    int phase = 0;
+    for (;; ++phase) {
+      if (phase == (int)phase_ranges.size()) phase_ranges.emplace_back();
+      bool clash = false;
+      for (const auto& r : mine)
+        for (const auto& o : phase_ranges[phase])
+          if (ranges_overlap(r.first, r.second, o.first, o.second)) clash = true;
+      if (!clash) break;
+    }
+    g.phase = phase;
+    for (const auto& r : mine) phase_ranges[phase].push_back(r);
+  }
+  return (int)phase_ranges.size();
+}
+
+}  // namespace
+
+void build_schedule(Plan& plan) {
+  const Spec& spec = plan.spec;
+
+  // ---- forward ----
+  plan.fwd_groups = make_groups(spec);
+  auto out_ranges = [](const Group& g) {
+    std::vector<std::pair<long, long>> r;
+    for (const auto& b : g.blocks) r.push_back({b.out_off, b.out_off + (long)g.channels * b.d3});
+    return r;
+  };
+  // Any overlap between blocks of different groups (or overlapping distinct
+  // blocks) means outputs are summed: zero-fill and accumulate everywhere.
+  std::vector<std::pair<long, long>> all;
+  for (const Group& g : plan.fwd_groups)
+    for (const auto& r : out_ranges(g)) all.push_back(r);
+  bool collision = false;
+  for (size_t a = 0; a < all.size(); ++a)
+    for (size_t b = a + 1; b < all.size(); ++b)
+      if (ranges_overlap(all[a].first, all[a].second, all[b].first, all[b].second)) collision = true;
+  std::vector<std::pair<long, long>> merged = all;
+  std::sort(merged.begin(), merged.end());
+  long covered = 0;
+  bool holes = false;
+  for (const auto& r : merged) {
+    if (r.first > covered) holes = true;
+    covered = std::max(covered, r.second);
+  }
+  if (covered < spec.out) holes = true;
+  plan.fwd_needs_zero = collision || holes;
+  for (Group& g : plan.fwd_groups)
+    for (auto& b : g.blocks) b.accumulate = collision;
+  plan.fwd_phases = assign_phases(plan.fwd_groups, out_ranges);
+  plan.phase_slots.assign(plan.fwd_phases, 0);
+  for (Group& g : plan.fwd_groups) {
+    g.slot_base = plan.phase_slots[g.phase];
+    plan.phase_slots[g.phase] += g.chunks;
+  }
+  for (int s : plan.phase_slots)
+    if (s > 65535) fail("too many channel chunks for one launch");
+
+  // ---- backward ----
+  plan.bwd_groups = plan.fwd_groups;
+  auto in_ranges = [](const Group& g) {
+    return std::vector<std::pair<long, long>>{{g.x_off, g.x_off + (long)g.channels * g.d1}};
+  };
+  std::vector<std::pair<long, long>> xs;
+  for (const Group& g : plan.bwd_groups) xs.push_back(in_ranges(g)[0]);
+  bool x_collision = false;
+  for (size_t a = 0; a < xs.size(); ++a)
+    for (size_t b = a + 1; b < xs.size(); ++b)
+      if (ranges_overlap(xs[a].first, xs[a].second, xs[b].first, xs[b].second)) x_collision = true;
+  std::sort(xs.begin(), xs.end());
+  covered = 0;
+  bool x_holes = false;
+  for (const auto& r : xs) {
+    if (r.first > covered) x_holes = true;
+    covered = std::max(covered, r.second);
+  }
+  if (covered < spec.in1) x_holes = true;
+  plan.bwd_gx_needs_zero = x_collision || x_holes;
+  for (Group& g : plan.bwd_groups) g.gx_accumulate = x_collision;
+  int bwd_phases = assign_phases(plan.bwd_groups, in_ranges);
+  // Backward phases reuse Group::phase; slots are numbered per phase, and
+  // gy partial slots are global.
+  std::vector<int> slots(bwd_phases, 0);
+  int parts = 0;
+  for (Group& g : plan.bwd_groups) {
+    g.slot_base = slots[g.phase];
+    slots[g.phase] += g.chunks;
+    g.gy_slot_base = parts;
+    parts += g.chunks;
+  }
+  plan.bwd_phases = bwd_phases;
+  plan.bwd_phase_slots = slots;
+  plan.gy_parts = parts;
+  for (int s : slots)
+    if (s > 65535) fail("too many channel chunks for one launch");
+}
+
+}  // namespace luna

@@ -1,0 +1,181 @@
+"""Graph validation and CSR tables shared by the convolution kernels.
+
+Restates ``make_graph`` / ``LunaTPGraph`` (``src/lunatp/graph.py:17-141``) and
+``make_source_segments`` (``src/lunatp/uvu_conv/graph.py:38-99``).  The tables
+are built with torch operations on the inputs' device; the edge permutation
+by source is a *stable* sort, so equal sources keep destination order and
+every table is deterministic.
+
+Tables (int32):
+  src, dst           copies of the inputs (the graph owns them)
+  dst_rowptr[N+1]    destination CSR over the dst-sorted edge list
+  src_rowptr[N+1]    source CSR over ``edge_ids_by_src``
+  edge_ids_by_src[E] edge ids ordered by source
+  edge_ids_by_dst[E] identity (edges are dst-sorted)
+  node_order[N]      nodes by descending in-degree (launch order, forward)
+  source_node_order  nodes by descending out-degree (launch order, backward)
+  node_tiers[3]      prefix lengths of node_order covering 1/4, 2/4, 3/4 of edges
+  source_segments    source-CSR chunks of at most 32 edges
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from operator import index
+
+import torch
+
+SOURCE_SEGMENT_EDGES = 32
+
+
+@dataclass(frozen=True)
+class SourceSegmentTables:
+    """Source-CSR segments of at most ``SOURCE_SEGMENT_EDGES`` edges.
+
+    ``nodes`` owns each segment, ``begin``/``end`` index ``edge_ids_by_src``,
+    ``rowptr`` maps a node to its segments and ``order`` is a launch permutation
+    (longest segments of the highest-degree nodes first).
+    """
+
+    nodes: torch.Tensor
+    begin: torch.Tensor
+    end: torch.Tensor
+    rowptr: torch.Tensor
+    order: torch.Tensor
+
+
+@dataclass(frozen=True)
+class LunaTPGraph:
+    """Prepared topology; tables are never modified after construction."""
+
+    src: torch.Tensor
+    dst: torch.Tensor
+    num_nodes: int
+    dst_rowptr: torch.Tensor
+    src_rowptr: torch.Tensor
+    edge_ids_by_src: torch.Tensor
+    edge_ids_by_dst: torch.Tensor
+    node_order: torch.Tensor | None = None
+    source_node_order: torch.Tensor | None = None
+    node_tiers: torch.Tensor | None = None
+    source_segments: SourceSegmentTables | None = None
+    _tables: dict = field(default_factory=dict, init=False, repr=False, compare=False)
+
+    @property
+    def num_edges(self) -> int:
+        return int(self.src.numel())
+
+    def to(self, device) -> "LunaTPGraph":
+        """Copy every table to ``device``."""
+        def move(t):
+            return None if t is None else t.to(device)
+        seg = self.source_segments
+        return LunaTPGraph(
+            src=move(self.src), dst=move(self.dst), num_nodes=self.num_nodes,
+            dst_rowptr=move(self.dst_rowptr), src_rowptr=move(self.src_rowptr),
+            edge_ids_by_src=move(self.edge_ids_by_src), edge_ids_by_dst=move(self.edge_ids_by_dst),
+            node_order=move(self.node_order), source_node_order=move(self.source_node_order),
+            node_tiers=move(self.node_tiers),
+            source_segments=None if seg is None else SourceSegmentTables(
+                *(move(t) for t in (seg.nodes, seg.begin, seg.end, seg.rowptr, seg.order))),
+        )
+
+
+def make_source_segments(src_rowptr: torch.Tensor) -> SourceSegmentTables:
+    """Split every source row into chunks of at most 32 edges (``uvu_conv/graph.py:38-99``).
+
+    Isolated nodes keep one empty segment so the segment CSR covers every node.
+    """
+    rowptr = src_rowptr.to(torch.int64)
+    degree = rowptr[1:] - rowptr[:-1]
+    count = ((degree + SOURCE_SEGMENT_EDGES - 1) // SOURCE_SEGMENT_EDGES).clamp_min(1)
+    seg_rowptr = torch.zeros(degree.numel() + 1, dtype=torch.int64, device=rowptr.device)
+    torch.cumsum(count, 0, out=seg_rowptr[1:])
+    total = int(seg_rowptr[-1].item())
+    nodes = torch.repeat_interleave(torch.arange(degree.numel(), device=rowptr.device), count,
+                                    output_size=total)
+    local = torch.arange(total, device=rowptr.device) - torch.repeat_interleave(
+        seg_rowptr[:-1], count, output_size=total)
+    begin = rowptr[nodes] + SOURCE_SEGMENT_EDGES * local
+    end = torch.minimum(begin + SOURCE_SEGMENT_EDGES, rowptr[nodes + 1])
+    by_degree = torch.argsort(degree[nodes], descending=True, stable=True)
+    order = by_degree[torch.argsort((end - begin)[by_degree], descending=True, stable=True)]
+    i32 = torch.int32
+    return SourceSegmentTables(nodes.to(i32), begin.to(i32), end.to(i32), seg_rowptr.to(i32), order.to(i32))
+
+
+def make_graph(src: torch.Tensor, dst: torch.Tensor, num_nodes: int | None = None) -> LunaTPGraph:
+    """Build the topology shared by all convolution layers.
+
+    ``src``/``dst`` are ``[edges]`` or ``[edges, 1]`` int32/int64 with ``dst``
+    sorted ascending; edge data must follow the same order.  Errors follow
+    ``src/lunatp/graph.py:64-98``.
+    """
+    if src.ndim == 2 and src.shape[1] == 1:
+        src = src.squeeze(-1)
+    if dst.ndim == 2 and dst.shape[1] == 1:
+        dst = dst.squeeze(-1)
+    if src.ndim != 1 or dst.ndim != 1 or src.shape != dst.shape:
+        raise ValueError("src and dst must have equal shape [edges] or [edges, 1].")
+    if src.dtype not in (torch.int32, torch.int64) or dst.dtype not in (torch.int32, torch.int64):
+        raise TypeError("graph indices must be int32 or int64.")
+    if num_nodes is not None and not isinstance(num_nodes, int):
+        num_nodes = index(num_nodes)
+    num_edges = src.numel()
+    required = 0
+    if num_edges:
+        src_min, src_max = torch.aminmax(src)
+        dst_min, dst_max = torch.aminmax(dst)
+        low = min(int(src_min), int(dst_min))
+        required = max(int(src_max), int(dst_max)) + 1
+        if low < 0:
+            raise ValueError("graph indices must be nonnegative.")
+        if num_edges > 1 and bool((dst[1:] < dst[:-1]).any()):
+            raise ValueError(
+                "dst must be sorted in ascending order; src and edge data must follow the same order.")
+    if num_nodes is None:
+        num_nodes = required
+    if num_nodes < required:
+        raise ValueError(
+            f"num_nodes={num_nodes} must be nonnegative and at least {required} for the supplied indices.")
+    if num_nodes >= (1 << 31):
+        raise OverflowError("graph node count exceeds signed int32 capacity.")
+    if num_edges >= (1 << 31) - 1:
+        raise OverflowError("graph edge count exceeds signed int32 capacity.")
+
+    device = src.device
+    i32 = torch.int32
+    src64, dst64 = src.to(torch.int64), dst.to(torch.int64)
+    src_deg = torch.bincount(src64, minlength=num_nodes)
+    dst_deg = torch.bincount(dst64, minlength=num_nodes)
+    src_rowptr = torch.zeros(num_nodes + 1, dtype=i32, device=device)
+    dst_rowptr = torch.zeros(num_nodes + 1, dtype=i32, device=device)
+    if num_nodes:
+        torch.cumsum(src_deg, 0, dtype=i32, out=src_rowptr[1:])
+        torch.cumsum(dst_deg, 0, dtype=i32, out=dst_rowptr[1:])
+    node_order = torch.argsort(dst_deg, descending=True, stable=True).to(i32)
+    source_node_order = torch.argsort(src_deg, descending=True, stable=True).to(i32)
+    if num_nodes and num_edges:
+        cumulative = dst_deg[node_order.long()].cumsum(0)
+        thresholds = torch.arange(1, 4, device=device, dtype=torch.int64) * num_edges // 4
+        node_tiers = (torch.searchsorted(cumulative, thresholds) + 1).to(i32)
+    else:
+        node_tiers = torch.full((3,), num_nodes, device=device, dtype=i32)
+    graph = LunaTPGraph(
+        src=src.to(dtype=i32, copy=True, memory_format=torch.contiguous_format),
+        dst=dst.to(dtype=i32, copy=True, memory_format=torch.contiguous_format),
+        num_nodes=num_nodes,
+        dst_rowptr=dst_rowptr,
+        src_rowptr=src_rowptr,
+        edge_ids_by_src=torch.argsort(src64, stable=True).to(i32),
+        edge_ids_by_dst=torch.arange(num_edges, device=device, dtype=i32),
+        node_order=node_order,
+        source_node_order=source_node_order,
+        node_tiers=node_tiers,
+        source_segments=make_source_segments(src_rowptr),
+    )
+    return graph
+
+
+__all__ = ["LunaTPGraph", "SourceSegmentTables", "make_graph", "make_source_segments",
+           "SOURCE_SEGMENT_EDGES"]

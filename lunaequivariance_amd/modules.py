@@ -1,0 +1,95 @@
+"""``TensorProductConv`` module (``src/modules/tensorproduct.py:119-206``)."""
+
+from __future__ import annotations
+
+from collections.abc import Mapping
+
+import torch
+
+from .graph import make_graph
+from .interface import tensor_product_conv
+from .layout import TensorProductConfig
+from .uvu_conv import create_uvu_conv_operator
+
+
+class TensorProductConv(torch.nn.Module):
+    """Fused tensor product on every edge, summed at destination nodes.
+
+    Pass irreps and instructions, an existing configuration (or e3nn-like
+    module with the same attributes), or prebuilt metadata with ``mode="uvu"``.
+    Build topology with ``create_graph`` and pass ``graph=`` on every call.
+    """
+
+    def __init__(self, irreps_in1, irreps_in2=None, irreps_out=None, instructions=None,
+                 in1_var=None, in2_var=None, out_var=None, irrep_normalization=None,
+                 path_normalization=None, internal_weights=None, shared_weights=None, *,
+                 dtype=None, mode=None):
+        super().__init__()
+        metadata = isinstance(irreps_in1, Mapping)
+        if metadata or isinstance(irreps_in1, torch.nn.Module):
+            if any(value is not None for value in (
+                    irreps_in2, irreps_out, instructions, in1_var, in2_var, out_var,
+                    irrep_normalization, path_normalization, internal_weights, shared_weights)):
+                raise TypeError(
+                    "Pass either an existing tensor product/metadata or irreps and path options")
+            tp = irreps_in1
+        else:
+            if irreps_in2 is None or irreps_out is None or instructions is None:
+                raise TypeError("irreps_in2, irreps_out and instructions are required")
+            tp = TensorProductConfig(
+                irreps_in1, irreps_in2, irreps_out, instructions,
+                in1_var=in1_var, in2_var=in2_var, out_var=out_var,
+                irrep_normalization=irrep_normalization, path_normalization=path_normalization,
+                internal_weights=internal_weights, shared_weights=shared_weights,
+            )
+            if dtype is not None and tp.weight.dtype != dtype:
+                tp.to(dtype=dtype)
+        if metadata:
+            if mode not in ("uuu", "uvu"):
+                raise ValueError('Prebuilt metadata requires mode="uuu" or mode="uvu"')
+            dtype = torch.float32 if dtype is None else dtype
+        else:
+            modes = {ins.connection_mode for ins in tp.instructions}
+            if len(modes) != 1 or not modes <= {"uuu", "uvu", "uvw"}:
+                raise ValueError("TensorProductConv requires one connection mode: uuu, uvu or uvw")
+            inferred = modes.pop()
+            if mode is not None and mode != inferred:
+                raise ValueError("mode must match the tensor-product instructions")
+            mode = inferred
+            weight = getattr(tp, "weight", None)
+            if dtype is None:
+                dtype = weight.dtype if isinstance(weight, torch.Tensor) else torch.get_default_dtype()
+        if mode != "uvu":
+            raise NotImplementedError(f"{mode} convolution is not part of this MI355X build")
+        self.mode = mode + "_conv"
+        self.op = create_uvu_conv_operator(tp, dtype=dtype)
+        if metadata:
+            self.weight_numel = tp["weight_numel"]
+            self.internal_weights = self.shared_weights = False
+        else:
+            self.tp = tp
+            self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
+            self.instructions = tp.instructions
+            self.weight_numel = tp.weight_numel
+            self.internal_weights, self.shared_weights = tp.internal_weights, tp.shared_weights
+
+    def _apply(self, fn, recurse=True):
+        dtype = fn(torch.empty(0, dtype=self.op.compute_dtype)).dtype
+        result = super()._apply(fn, recurse=recurse)
+        if dtype in (torch.float32, torch.float64) and dtype != self.op.compute_dtype:
+            self.op = create_uvu_conv_operator(self.op.meta if not hasattr(self, "tp") else self.tp,
+                                               dtype=dtype)
+        return result
+
+    @staticmethod
+    def create_graph(src, dst, num_nodes=None, **kwargs):
+        """Prepare shared topology once per batch."""
+        return make_graph(src, dst, num_nodes, **kwargs)
+
+    def forward(self, x, edge_attr, weight=None, *, graph, **kwargs):
+        if weight is None and self.internal_weights:
+            weight = self.tp.weight
+        return tensor_product_conv(x, edge_attr, weight, graph=graph, config=self.op, **kwargs)
+
+
+__all__ = ["TensorProductConv"]

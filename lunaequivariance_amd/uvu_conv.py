@@ -1,0 +1,416 @@
+"""UVU tensor-product convolution: metadata lowering, operator and autograd.
+
+Lowering follows ``build_uvu_conv_metadata``
+(``src/lunatp/uvu_conv/kernels/utils.py:23-119``): every instruction and every
+edge channel ``v`` becomes one path spec with offsets into x, y, out and the
+per-edge weight row (``w[e, weight_offset + u * weight_stride]``, e3nn's
+``[input_channel, edge_channel]`` layout), and sparse coefficient terms
+``(i, j, k, cg * path_weight)``.
+
+The operator hands the specs to the C-ABI library, which emits and compiles
+gfx950 kernels for exactly this path set.  Autograd is built from two
+differentiable primitives, the forward and the first-order backward
+(``UVUConvForward``/``UVUConvBackward``, ``src/lunatp/uvu_conv/interface.py:210-348``).
+Because the convolution is multilinear in (x, y, w, env) and linear in the
+output seeds, every higher derivative is a sum of these two primitives with
+some arguments replaced by their cotangents, so second and third order
+derivatives run on the same kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from math import prod
+
+import torch
+
+from . import _native
+from .cg import sparse_terms
+from .graph import LunaTPGraph
+from .layout import TensorProductPaths
+
+
+def build_uvu_conv_metadata(tp, coefficient_dtype=torch.float32) -> dict:
+    """Path specs of a UVU configuration (``uvu_conv/kernels/utils.py:23-119``)."""
+    if coefficient_dtype not in (torch.float32, torch.float64):
+        raise ValueError(
+            f"UVU convolution coefficients require float32 or float64; got {coefficient_dtype}.")
+    if tp.internal_weights:
+        raise ValueError("Generated SO3 kernels require internal_weights=False.")
+    if tp.shared_weights:
+        raise ValueError("Generated SO3 kernels require shared_weights=False.")
+    in_slices = tp.irreps_in1.slices()
+    edge_slices = tp.irreps_in2.slices()
+    out_slices = tp.irreps_out.slices()
+    specs = []
+    weight_offset = 0
+    max_channels = 0
+    for index, ins in enumerate(tp.instructions):
+        if ins.connection_mode != "uvu":
+            raise ValueError(f"Only connection_mode='uvu' is supported, got {ins.connection_mode!r}.")
+        if not ins.has_weight:
+            raise ValueError("Generated SO3 kernels require weighted uvu instructions.")
+        mul_in, ir_in = tp.irreps_in1[ins.i_in1]
+        mul_edge, ir_edge = tp.irreps_in2[ins.i_in2]
+        mul_out, ir_out = tp.irreps_out[ins.i_out]
+        if mul_in != mul_out:
+            raise ValueError(
+                f"UVU requires equal input/output multiplicities; got {mul_in} and {mul_out} "
+                f"for path ({ins.i_in1}, {ins.i_in2}, {ins.i_out}).")
+        if tuple(ins.path_shape) != (mul_in, mul_edge):
+            raise ValueError(f"UVU expects path_shape=({mul_in}, {mul_edge}); got {ins.path_shape}.")
+        max_channels = max(max_channels, mul_in)
+        terms = sparse_terms(ir_in.l, ir_edge.l, ir_out.l, float(ins.path_weight))
+        if coefficient_dtype == torch.float32:
+            terms = [(i, j, k, float(torch.tensor(c, dtype=torch.float32))) for i, j, k, c in terms]
+        for v in range(mul_edge):
+            spec = {
+                "x_offset": in_slices[ins.i_in1].start,
+                "y_offset": edge_slices[ins.i_in2].start + v * ir_edge.dim,
+                "out_offset": out_slices[ins.i_out].start,
+                "weight_offset": weight_offset + v,
+                "channels": mul_in,
+                "d1": ir_in.dim, "d2": ir_edge.dim, "d3": ir_out.dim,
+                "l1": ir_in.l, "l2": ir_edge.l, "l3": ir_out.l,
+                "terms": terms,
+            }
+            if mul_edge != 1:
+                spec["weight_stride"] = mul_edge
+                spec["l0_path"] = index
+            specs.append(spec)
+        weight_offset += prod(ins.path_shape)
+    if not specs:
+        raise ValueError("No uvu instructions found.")
+    if weight_offset != tp.weight_numel:
+        raise ValueError(
+            f"Lowered weight_numel={weight_offset}, but configuration reports {tp.weight_numel}.")
+    return {
+        "in1_dim": tp.irreps_in1.dim,
+        "in2_dim": tp.irreps_in2.dim,
+        "out_dim": tp.irreps_out.dim,
+        "weight_numel": tp.weight_numel,
+        "max_channels": max_channels,
+        "generated_specs": specs,
+    }
+
+
+def l0_feature_layout(specs) -> tuple[dict, int]:
+    """Column of each scalar-output path in the l0 feature matrix (``layout.py:150-170``).
+
+    Edge copies of one instruction share a column block; paths are ordered by
+    output offset.
+    """
+    offsets, keyed, width = {}, {}, 0
+    for index, spec in sorted(enumerate(specs), key=lambda item: int(item[1]["out_offset"])):
+        if int(spec["l3"]) != 0:
+            continue
+        key = ("instruction", int(spec["l0_path"])) if "l0_path" in spec else ("path", index)
+        if key not in keyed:
+            keyed[key] = width
+            width += int(spec["channels"])
+        offsets[index] = keyed[key]
+    return offsets, width
+
+
+def spec_text(meta: dict, dtype: torch.dtype) -> str:
+    """Serialise path specs into the C-ABI's plan specification."""
+    specs = meta["generated_specs"]
+    offsets, l0_dim = l0_feature_layout(specs)
+    bits = 64 if dtype == torch.float64 else 32
+    parts = [f"LUNAUVU1 {bits} {meta['in1_dim']} {meta['in2_dim']} {meta['out_dim']} "
+             f"{meta['weight_numel']} {len(specs)} {l0_dim}"]
+    for index, spec in enumerate(specs):
+        terms = spec["terms"]
+        head = (f"{spec['x_offset']} {spec['y_offset']} {spec['out_offset']} {spec['weight_offset']} "
+                f"{int(spec.get('weight_stride', 1))} {spec['channels']} {spec['d1']} {spec['d2']} "
+                f"{spec['d3']} {offsets.get(index, -1)} {len(terms)}")
+        body = " ".join(f"{int(i)} {int(j)} {int(k)} {float(c)!r}" for i, j, k, c in terms)
+        parts.append(head + (" " + body if body else ""))
+    return "\n".join(parts) + "\n"
+
+
+class NativePlan:
+    """Owner of one C-ABI plan handle."""
+
+    def __init__(self, text: str):
+        lib = _native.lib()
+        handle = ctypes.c_void_p()
+        _native.check(lib.luna_uvu_plan_create(text.encode(), _native.cache_dir().encode(),
+                                               ctypes.byref(handle)), "luna_uvu_plan_create")
+        self.handle = handle
+        info = _native.PlanInfo()
+        _native.check(lib.luna_uvu_plan_info(handle, ctypes.byref(info)), "luna_uvu_plan_info")
+        self.info = info
+
+    def precompile(self):
+        _native.check(_native.lib().luna_uvu_plan_precompile(self.handle), "luna_uvu_plan_precompile")
+
+    def __del__(self):
+        handle = getattr(self, "handle", None)
+        if handle is not None and _native._lib is not None:
+            _native._lib.luna_uvu_plan_destroy(handle)
+            self.handle = None
+
+
+class LunaTPUVUConv:
+    """Prepared UVU convolution (``src/lunatp/interface.py:353-367``)."""
+
+    mode = "uvu_conv"
+    index_mode = "uvu_conv"
+
+    def __init__(self, meta, *, dtype=torch.float32, index_bits=32):
+        if dtype not in (torch.float32, torch.float64):
+            raise ValueError("LunaTP uvu_conv requires torch.float32 or torch.float64.")
+        if index_bits != 32:
+            raise ValueError("only 32-bit graph indexing is supported")
+        self.meta = dict(meta)
+        self.compute_dtype = dtype
+        self.index_bits = index_bits
+        self.in1_dim = int(meta["in1_dim"])
+        self.in2_dim = int(meta["in2_dim"])
+        self.out_dim = int(meta["out_dim"])
+        self.weight_numel = int(meta["weight_numel"])
+        self.max_channels = int(meta["max_channels"])
+        self.generated_specs = list(meta["generated_specs"])
+        self.l0_offsets, self.l0_dim = l0_feature_layout(self.generated_specs)
+        self.spec = spec_text(self.meta, dtype)
+        self._plan = None
+
+    @property
+    def plan(self) -> NativePlan:
+        if self._plan is None:
+            self._plan = NativePlan(self.spec)
+        return self._plan
+
+    def run(self, x, edge_attr, weight, *, graph, env=None, return_l0_feat=False):
+        return lunatp_uvu_conv_func(self, x, edge_attr, weight, graph=graph, env=env,
+                                    return_l0_feat=return_l0_feat)
+
+    def __getstate__(self):
+        state = dict(self.__dict__)
+        state["_plan"] = None
+        return state
+
+
+def create_uvu_conv_operator(tp_or_meta, *, dtype=None):
+    """Prepared operator from a configuration or from prebuilt metadata."""
+    from collections.abc import Mapping
+
+    if not isinstance(tp_or_meta, Mapping):
+        tp_or_meta = TensorProductPaths.from_tensor_product(tp_or_meta)
+    if dtype is None:
+        dtype = torch.float32
+    elif dtype is not torch.float32 and dtype is not torch.float64:
+        raise ValueError("LunaTP uvu_conv requires torch.float32 or torch.float64.")
+    meta = tp_or_meta if isinstance(tp_or_meta, Mapping) else build_uvu_conv_metadata(tp_or_meta, dtype)
+    if not meta["generated_specs"] or any(int(s["channels"]) <= 0 for s in meta["generated_specs"]):
+        raise ValueError("UVU convolution requires positive channels for every path")
+    return LunaTPUVUConv(meta, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# Kernel calls (no autograd)
+# ---------------------------------------------------------------------------
+
+def _stream(tensor) -> int:
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def _check_device(op, graph, *tensors):
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("UVU convolution kernels run on the GPU; got a CPU tensor")
+        if t.dtype != op.compute_dtype:
+            raise TypeError(f"expected {op.compute_dtype}, got {t.dtype}")
+    if not graph.src.is_cuda:
+        raise RuntimeError("graph tables must live on the GPU; build the graph from GPU tensors")
+
+
+def run_forward(op, x, y, w, graph, env=None, want_l0=False):
+    """out [N, out_dim] (and l0 [E, l0_dim]) from the forward kernel."""
+    _check_device(op, graph, x, y, w, env)
+    N, E = graph.num_nodes, graph.num_edges
+    if x.shape != (N, op.in1_dim):
+        raise ValueError(f"x must have shape ({N}, {op.in1_dim}); got {tuple(x.shape)}")
+    if y.shape != (E, op.in2_dim) or w.shape != (E, op.weight_numel):
+        raise ValueError("edge_attr/weight rows must match the graph's edges")
+    plan = op.plan
+    factory = torch.zeros if plan.info.fwd_needs_zero else torch.empty
+    out = factory((N, op.out_dim), device=x.device, dtype=x.dtype)
+    l0 = None
+    if want_l0:
+        l0 = torch.empty((E, op.l0_dim), device=x.device, dtype=x.dtype)
+    if N:
+        _native.check(_native.lib().luna_uvu_conv_fwd(
+            plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w), _native.ptr(env),
+            graph.src.data_ptr(), graph.dst_rowptr.data_ptr(), graph.node_order.data_ptr(),
+            out.data_ptr(), _native.ptr(l0) if (l0 is not None and l0.numel()) else None,
+            N, E, _stream(x)), "luna_uvu_conv_fwd")
+    return out, l0
+
+
+def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, True, True)):
+    """(gx, gy, gw, genv) from the first-order backward kernels."""
+    _check_device(op, graph, x, y, w, env, g, gl0)
+    N, E = graph.num_nodes, graph.num_edges
+    plan = op.plan
+    need_x, need_y, need_w, need_env = needs
+    need_env = need_env and env is not None
+    gx = gy = gw = genv = None
+    if need_x:
+        factory = torch.zeros if plan.info.bwd_gx_needs_zero else torch.empty
+        gx = factory((N, op.in1_dim), device=x.device, dtype=x.dtype)
+    if need_y:
+        gy = torch.empty((E, op.in2_dim), device=x.device, dtype=x.dtype)
+    if need_w:
+        gw = torch.empty((E, op.weight_numel), device=x.device, dtype=x.dtype)
+    if need_env:
+        genv = torch.empty((E,), device=x.device, dtype=x.dtype)
+    if N and (need_x or ((need_y or need_w or need_env) and E)):
+        lib = _native.lib()
+        size = ctypes.c_size_t()
+        _native.check(lib.luna_uvu_conv_bwd_workspace(plan.handle, N, E, ctypes.byref(size)),
+                      "luna_uvu_conv_bwd_workspace")
+        workspace = None
+        if (need_y or need_env) and E:
+            workspace = torch.empty(size.value, device=x.device, dtype=torch.uint8)
+        _native.check(lib.luna_uvu_conv_bwd(
+            plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w), _native.ptr(env),
+            g.data_ptr(), _native.ptr(gl0) if (gl0 is not None and gl0.numel()) else None,
+            graph.dst.data_ptr(), graph.src_rowptr.data_ptr(), graph.edge_ids_by_src.data_ptr(),
+            graph.source_node_order.data_ptr(),
+            _native.ptr(gx), _native.ptr(gy), _native.ptr(gw), _native.ptr(genv),
+            _native.ptr(workspace), size.value if workspace is not None else 0,
+            N, E, _stream(x)), "luna_uvu_conv_bwd")
+    if gy is not None and not E:
+        gy.zero_()
+    return gx, gy, gw, genv
+
+
+# ---------------------------------------------------------------------------
+# Autograd
+# ---------------------------------------------------------------------------
+
+def _contig(t):
+    return None if t is None else t.contiguous()
+
+
+def _add(a, b):
+    if a is None:
+        return b
+    if b is None:
+        return a
+    return a + b
+
+
+class UVUConvForward(torch.autograd.Function):
+    """Differentiable forward; its backward is ``UVUConvBackward``."""
+
+    @staticmethod
+    def forward(ctx, op, graph, want_l0, x, y, w, env):
+        ctx.op, ctx.graph, ctx.want_l0 = op, graph, want_l0
+        ctx.save_for_backward(x, y, w, env)
+        ctx.set_materialize_grads(False)
+        out, l0 = run_forward(op, x, y, w, graph, env, want_l0)
+        if want_l0:
+            return out, l0
+        return out
+
+    @staticmethod
+    def backward(ctx, g, gl0=None):
+        x, y, w, env = ctx.saved_tensors
+        op, graph = ctx.op, ctx.graph
+        if g is None and gl0 is None:
+            return None, None, None, None, None, None, None
+        if g is None:
+            g = x.new_zeros((graph.num_nodes, op.out_dim))
+        needs = ctx.needs_input_grad
+        gx, gy, gw, genv = conv_backward(op, graph, x, y, w, env, _contig(g), _contig(gl0),
+                                         needs=(needs[3], needs[4], needs[5], needs[6]))
+        return None, None, None, gx, gy, gw, genv
+
+
+def conv_forward(op, graph, want_l0, x, y, w, env):
+    """Differentiable forward used by the higher-order rules."""
+    return UVUConvForward.apply(op, graph, want_l0, x, y, w, env)
+
+
+class UVUConvBackward(torch.autograd.Function):
+    """Differentiable first-order backward: (x, y, w, env, g, gl0) -> (gx, gy, gw, genv)."""
+
+    @staticmethod
+    def forward(ctx, op, graph, needs, x, y, w, env, g, gl0):
+        ctx.op, ctx.graph = op, graph
+        ctx.save_for_backward(x, y, w, env, g, gl0)
+        ctx.set_materialize_grads(False)
+        return run_backward(op, x, y, w, graph, g, env, gl0, needs)
+
+    @staticmethod
+    def backward(ctx, rx, ry, rw, renv):
+        x, y, w, env, g, gl0 = ctx.saved_tensors
+        op, graph = ctx.op, ctx.graph
+        need = ctx.needs_input_grad  # (op, graph, needs, x, y, w, env, g, gl0)
+        want_l0 = gl0 is not None
+        # Multilinear arguments and their cotangent directions.
+        args = [x, y, w, env]
+        dirs = [_contig(rx), _contig(ry), _contig(rw), _contig(renv) if env is not None else None]
+        grads = [None, None, None, None]
+        hg = hl0 = None
+        for slot, direction in enumerate(dirs):
+            if direction is None:
+                continue
+            substituted = list(args)
+            substituted[slot] = direction
+            # The scalar features do not depend on env: an env direction moves
+            # only the node output, and the gl0 seed drops out of its terms.
+            scalar = want_l0 and slot != 3
+            if need[7] or (need[8] and scalar):
+                result = conv_forward(op, graph, scalar, *substituted)
+                if scalar:
+                    out, l0 = result
+                    hl0 = _add(hl0, l0)
+                else:
+                    out = result
+                hg = _add(hg, out)
+            wanted = tuple(need[3 + other] and other != slot and args[other] is not None
+                           for other in range(4))
+            if any(wanted):
+                parts = conv_backward(op, graph, *substituted, g, gl0 if slot != 3 else None,
+                                      needs=wanted)
+                for other in range(4):
+                    if wanted[other] and parts[other] is not None:
+                        grads[other] = _add(grads[other], parts[other])
+        return (None, None, None, grads[0], grads[1], grads[2], grads[3],
+                hg if need[7] else None, hl0 if need[8] else None)
+
+
+def conv_backward(op, graph, x, y, w, env, g, gl0, needs=(True, True, True, True)):
+    needs = tuple(bool(n) for n in needs)
+    if torch.is_grad_enabled():
+        return UVUConvBackward.apply(op, graph, needs, x, y, w, env, g, gl0)
+    return run_backward(op, x, y, w, graph, g, env, gl0, needs)
+
+
+def lunatp_uvu_conv_func(op, x, edge_attr, weight, *, graph: LunaTPGraph, env=None,
+                         return_l0_feat=False):
+    """Aggregate UVU edge messages at destination nodes (``uvu_conv/interface.py:143-204``).
+
+    x [num_nodes, in1_dim], edge_attr [num_edges, in2_dim], weight
+    [num_edges, weight_numel], env [num_edges] or [num_edges, 1].  Returns
+    out [num_nodes, out_dim], or (out, l0_feat [num_edges, l0_dim]).
+    """
+    if weight is None:
+        raise ValueError("UVU convolution requires explicit per-edge weights")
+    x = x.contiguous()
+    edge_attr = edge_attr.contiguous()
+    weight = weight.contiguous()
+    if env is not None:
+        env = env.reshape(-1).contiguous()
+    return UVUConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
+
+
+__all__ = ["build_uvu_conv_metadata", "l0_feature_layout", "spec_text", "LunaTPUVUConv",
+           "create_uvu_conv_operator", "lunatp_uvu_conv_func", "run_forward", "run_backward",
+           "NativePlan"]

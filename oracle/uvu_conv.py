@@ -1,0 +1,144 @@
+"""Dense fp64 restatement of the reference's oracle for the UVU convolution.
+
+The reference checks its kernels against e3nn's ``o3.TensorProduct`` applied
+to ``x[src]`` followed by ``index_add`` over ``dst``
+(``src/utils/testing.py:12-70``, ``tests/lunatp/test_uvu_conv.py:37-41``), with
+the operation documented in ``docs/operators/tensor_product_conv.md``
+("Equivalent e3nn computation").  For a uvu instruction ``(i1, i2, io)`` with
+normalised path weight ``pw`` (``src/lunatp/utils/layout.py:323-370``) and edge
+multiplicity ``m2``:
+
+    msg[e, io][u, k] = pw * sum_{v, i, j} C[i, j, k] x[src_e, i1][u, i]
+                                          y[e, i2][v, j] w[e, off + u*m2 + v]
+    out[n] = sum_{e: dst_e = n} env_e * msg[e]
+
+and the scalar-path features (``src/utils/testing.py:55-70``) are the per-edge
+``msg`` columns of instructions whose output has l = 0, before ``env``,
+concatenated in output order.  Everything is differentiable torch fp64 code,
+so gradients of any order come from autograd.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from .wigner import wigner_3j
+
+
+def parse_irreps(text: str):
+    """[(mul, l, parity)] of an e3nn irreps string."""
+    out = []
+    for chunk in text.replace(" ", "").split("+"):
+        if not chunk:
+            continue
+        mul, ir = chunk.split("x") if "x" in chunk else ("1", chunk)
+        out.append((int(mul), int(ir[:-1]), 1 if ir[-1] == "e" else -1))
+    return out
+
+
+def path_weights(in1, in2, out, instructions, irrep_normalization="component",
+                 path_normalization="element"):
+    """sqrt(alpha) per instruction (``layout.py:323-370``), unit variances."""
+    weights = []
+    for i1, i2, io, mode, _has_w, *rest in instructions:
+        user = rest[0] if rest else 1.0
+        l1, l2, l3 = in1[i1][1], in2[i2][1], out[io][1]
+        alpha = {"component": 2 * l3 + 1, "norm": (2 * l1 + 1) * (2 * l2 + 1), "none": 1}[irrep_normalization]
+        fan = lambda ins: {"uvu": in2[ins[1]][0], "uvw": in1[ins[0]][0] * in2[ins[1]][0], "uuu": 1}[ins[3]]
+        if path_normalization == "element":
+            x = sum(fan(other) for other in instructions if other[2] == io)
+        elif path_normalization == "path":
+            x = fan((i1, i2, io, mode)) * sum(1 for other in instructions if other[2] == io)
+        else:
+            x = 1
+        if x > 0:
+            alpha /= x
+        weights.append(math.sqrt(alpha * user))
+    return weights
+
+
+def offsets(irreps):
+    out, start = [], 0
+    for mul, l, _ in irreps:
+        out.append(start)
+        start += mul * (2 * l + 1)
+    return out, start
+
+
+def edge_messages(in1, in2, out, instructions, x_src, y, w, weights=None):
+    """Per-edge messages [E, out_dim] and the per-instruction output pieces."""
+    if weights is None:
+        weights = path_weights(in1, in2, out, instructions)
+    x_off, _ = offsets(in1)
+    y_off, _ = offsets(in2)
+    o_off, out_dim = offsets(out)
+    E = y.shape[0]
+    pieces = []
+    w_off = 0
+    msg = x_src.new_zeros((E, out_dim))
+    for (i1, i2, io, mode, _has_w, *_), pw in zip(instructions, weights):
+        if mode != "uvu":
+            raise ValueError("oracle covers uvu instructions")
+        m1, l1, _ = in1[i1]
+        m2, l2, _ = in2[i2]
+        mo, l3, _ = out[io]
+        d1, d2, d3 = 2 * l1 + 1, 2 * l2 + 1, 2 * l3 + 1
+        cg = torch.tensor(wigner_3j(l1, l2, l3), dtype=x_src.dtype)
+        xb = x_src[:, x_off[i1]: x_off[i1] + m1 * d1].reshape(E, m1, d1)
+        yb = y[:, y_off[i2]: y_off[i2] + m2 * d2].reshape(E, m2, d2)
+        wb = w[:, w_off: w_off + m1 * m2].reshape(E, m1, m2)
+        piece = pw * torch.einsum("ijk,eui,evj,euv->euk", cg, xb, yb, wb).reshape(E, mo * d3)
+        pieces.append((io, piece))
+        msg = msg + torch.nn.functional.pad(piece, (o_off[io], out_dim - o_off[io] - mo * d3))
+        w_off += m1 * m2
+    return msg, pieces
+
+
+def uvu_conv(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, dst, num_nodes,
+             env=None, return_l0=False):
+    """Reference semantics of ``TensorProductConv(...)(x, y, w, graph=..., env=, return_l0_feat=)``."""
+    in1, in2, out = parse_irreps(irreps_in1), parse_irreps(irreps_in2), parse_irreps(irreps_out)
+    src = torch.as_tensor(src).long()
+    dst = torch.as_tensor(dst).long()
+    msg, pieces = edge_messages(in1, in2, out, instructions, x[src], y, w)
+    scaled = msg if env is None else msg * env.reshape(-1, 1)
+    result = x.new_zeros((num_nodes, msg.shape[1])).index_add(0, dst, scaled)
+    if not return_l0:
+        return result
+    scalars = sorted([(io, piece) for io, piece in pieces if out[io][1] == 0], key=lambda t: t[0])
+    l0 = torch.cat([p for _, p in scalars], 1) if scalars else msg[:, :0]
+    return result, l0
+
+
+def brute_force(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, dst, num_nodes):
+    """Scalar loop version of ``uvu_conv`` for tiny problems (pins the einsum form)."""
+    in1, in2, out = parse_irreps(irreps_in1), parse_irreps(irreps_in2), parse_irreps(irreps_out)
+    weights = path_weights(in1, in2, out, instructions)
+    x_off, _ = offsets(in1)
+    y_off, _ = offsets(in2)
+    o_off, out_dim = offsets(out)
+    x, y, w = (np.asarray(t, dtype=np.float64) for t in (x, y, w))
+    result = np.zeros((num_nodes, out_dim))
+    for e in range(len(src)):
+        w_off = 0
+        for (i1, i2, io, _m, _h, *_), pw in zip(instructions, weights):
+            m1, l1, _ = in1[i1]
+            m2, l2, _ = in2[i2]
+            _, l3, _ = out[io]
+            cg = wigner_3j(l1, l2, l3)
+            for u in range(m1):
+                for v in range(m2):
+                    for i in range(2 * l1 + 1):
+                        for j in range(2 * l2 + 1):
+                            for k in range(2 * l3 + 1):
+                                c = cg[i, j, k]
+                                if c == 0.0:
+                                    continue
+                                result[dst[e], o_off[io] + u * (2 * l3 + 1) + k] += (
+                                    pw * c * x[src[e], x_off[i1] + u * (2 * l1 + 1) + i]
+                                    * y[e, y_off[i2] + v * (2 * l2 + 1) + j] * w[e, w_off + u * m2 + v])
+            w_off += m1 * m2
+    return result
