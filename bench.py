@@ -1,0 +1,200 @@
+"""Benchmark of the fused UVU TensorProductConv on one MI355X.
+
+Default workload (config 2 of the benchmark contract): MACE-style lmax=3 UVU
+interaction, 128 channels, fp32, 20,000 atoms at 0.1 atoms/A^3 in a periodic
+cube, radius graph with a 5 A cutoff (~1.05M edges, dst-sorted), edge
+attributes = real spherical harmonics l<=3 of the edge vectors, per-edge
+weights ~ N(0,1)/sqrt(34).  One step = forward + backward to x, edge_attr and
+weight through the public module and autograd, inputs resident in HBM.
+
+Prints ONE JSON line: edges/s for the whole step, plus the roofline of the
+dominant kernel (algorithmic bytes per launch / its average launch time from
+HIP events recorded on the launch stream) and a CPU baseline (the fp32 torch
+restatement in ``oracle/`` on a bounded shard of the same workload, timed on
+this host's cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP64_PEAK_TFLOPS = 78.6
+
+CONFIGS = {
+    "cfg2": dict(channels=128, atoms=20000, dtype="float32", double_backward=False),
+    "cfg3": dict(channels=128, atoms=20000, dtype="float64", double_backward=False),
+    "cfg4": dict(channels=64, atoms=10000, dtype="float32", double_backward=True),
+}
+
+
+def parse_args():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-shard", type=int, default=400,
+                        help="CPU baseline runs 1/shard of the destination rows")
+    return parser.parse_args()
+
+
+def algorithmic_bytes(N, E, in1, in2, out, wnum, real, index=4):
+    """Compulsory bytes per launch: each tensor read or written once."""
+    X, Y, W, O = N * in1 * real, E * in2 * real, E * wnum * real, N * out * real
+    fwd = X + Y + W + O + E * index + (N + 1) * index
+    bwd_main = (X + Y + W + O) + (X + W) + 2 * E * index + (N + 1) * index
+    return {"uvu_fwd_p0": fwd, "uvu_bwd_p0": bwd_main, "uvu_bwd_reduce": Y}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the operator shards by destination-node ranges; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import lunaequivariance_amd as lunaeq
+    from lunaequivariance_amd import _native
+    from lunaequivariance_amd.workloads import mace_irreps, periodic_radius_graph, spherical_harmonics
+
+    cfg = CONFIGS[args.config]
+    dtype = getattr(torch, cfg["dtype"])
+    real = torch.finfo(dtype).bits // 8
+    device = torch.device("cuda:0")
+    torch.manual_seed(0)
+
+    in1, sh, out_irreps, instructions = mace_irreps(cfg["channels"], 3)
+    conv = lunaeq.TensorProductConv(in1, sh, out_irreps, instructions, internal_weights=False,
+                                    shared_weights=False, dtype=dtype)
+    N = cfg["atoms"]
+    src, dst, _pos, vec, _box = periodic_radius_graph(N, 0.1, 5.0, seed=0, device=device)
+    E = src.numel()
+    graph = conv.create_graph(src, dst, N)
+    fan_in = len(instructions)
+    x = torch.randn(N, conv.irreps_in1.dim, device=device, dtype=dtype, requires_grad=True)
+    y = spherical_harmonics(3, vec).to(dtype).requires_grad_()
+    w = (torch.randn(E, conv.weight_numel, device=device, dtype=dtype) / fan_in ** 0.5).requires_grad_()
+    g = torch.randn(N, conv.irreps_out.dim, device=device, dtype=dtype)
+    del vec
+
+    def step():
+        out = conv(x, y, w, graph=graph)
+        if cfg["double_backward"]:
+            gx, gy, gw = torch.autograd.grad(out, (x, y, w), g, create_graph=True)
+            ry = torch.randn_like(gy)
+            second = torch.autograd.grad(gy, (x, w), ry)
+            return out, gx, gy, gw, second
+        return (out, *torch.autograd.grad(out, (x, y, w), g))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _native.profile_enable(True)
+    _native.profile_collect()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        result = step()
+        del result
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    _native.profile_enable(False)
+    kernels = _native.profile_collect()
+    ms_per_step = elapsed * 1000.0 / args.steps
+    value = E / (ms_per_step / 1000.0)
+
+    algo = algorithmic_bytes(N, E, conv.irreps_in1.dim, conv.irreps_in2.dim, conv.irreps_out.dim,
+                             conv.weight_numel, real)
+    per_kernel = {}
+    for name, (count, total_ms, low, high) in kernels.items():
+        avg = total_ms / count
+        entry = {"launches": count, "avg_ms": round(avg, 4), "min_ms": round(low, 4),
+                 "max_ms": round(high, 4)}
+        if name in algo and not cfg["double_backward"]:
+            entry["algorithmic_bytes"] = algo[name]
+            entry["gbs"] = round(algo[name] / (avg / 1000.0) / 1e9, 1)
+        per_kernel[name] = entry
+    dominant = max(kernels, key=lambda n: kernels[n][1]) if kernels else None
+    roofline = None
+    if dominant and "gbs" in per_kernel[dominant]:
+        achieved = per_kernel[dominant]["gbs"]
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    step_bytes = algo["uvu_fwd_p0"] + algo["uvu_bwd_p0"] + algo["uvu_bwd_reduce"]
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, args.cpu_shard,
+                           dtype)
+
+    line = {
+        "metric": "UVU TP-conv edges/s fwd+bwd",
+        "value": round(value, 1),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if dtype == torch.float32 else "f64",
+        "data": "synthetic (periodic random atoms, radius graph, SH edge attributes, random weights)",
+        "config": {"workload": f"{args.config}: MACE-style UVU conv lmax=3, {cfg['channels']} channels, "
+                               f"{N} atoms, radius 5A, density 0.1"
+                               + (", fwd+bwd+double-bwd(gy)" if cfg["double_backward"] else ", fwd+bwd"),
+                   "num_nodes": N, "num_edges": E, "channels": cfg["channels"],
+                   "weight_numel": conv.weight_numel, "parallelism": "single GPU"},
+        "step_algorithmic_gb": round(step_bytes / 1e9, 3),
+        "step_hbm_frac": round(step_bytes / (ms_per_step / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)
+        if not cfg["double_backward"] else None,
+        "roofline": roofline,
+        "kernels": per_kernel,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, shard, dtype):
+    """The oracle's fp32 torch restatement, fwd+bwd, on the edges of the first N/shard
+    destination rows (contiguous in the dst-sorted edge list)."""
+    import torch
+
+    from oracle.uvu_conv import uvu_conv
+
+    rows = max(1, N // shard)
+    dst_cpu = dst.cpu()
+    count = int((dst_cpu < rows).sum())
+    xs = x.detach().cpu().clone().requires_grad_()
+    ys = y.detach()[:count].cpu().clone().requires_grad_()
+    ws = w.detach()[:count].cpu().clone().requires_grad_()
+    gs = g[:rows].cpu()
+    srcs, dsts = src[:count].cpu(), dst_cpu[:count]
+    threads = torch.get_num_threads()
+    times = []
+    for repeat in range(4):
+        start = time.perf_counter()
+        out = uvu_conv(in1, sh, out_irreps, instructions, xs, ys, ws, srcs, dsts, rows)
+        torch.autograd.grad(out, (xs, ys, ws), gs)
+        times.append(time.perf_counter() - start)
+    timed = times[1:]
+    return {"value": round(count / statistics.median(timed), 1), "unit": "edges/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{count} edges into the first {rows} of {N} destination rows (1/{shard}), "
+                      f"fwd+bwd, median of {len(timed)} after 1 warm-up, {str(dtype).split('.')[-1]}"}
+
+
+if __name__ == "__main__":
+    main()

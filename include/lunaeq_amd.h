@@ -51,7 +51,7 @@ typedef struct LunaUvuPlanInfo {
   int32_t in1_dim, in2_dim, out_dim, weight_numel, l0_dim;
   int32_t num_paths;
   int32_t fwd_needs_zero;    /* out must be zero-filled before luna_uvu_conv_fwd */
-  int32_t bwd_gx_needs_zero; /* gx must be zero-filled before luna_uvu_conv_bwd */
+  int32_t bwd_gx_needs_zero; /* input blocks overlap: gx messages are accumulated */
   int32_t num_fwd_launches;  /* launches per forward call */
   int32_t gy_parts;          /* partial slots of the edge-attribute gradient */
 } LunaUvuPlanInfo;
@@ -112,18 +112,31 @@ int luna_uvu_conv_bwd_workspace(const LunaUvuPlan* plan, int64_t num_nodes,
  * First-order backward.  g = dL/dout [N, out_dim]; gl0 = dL/dl0 [E, l0_dim] or
  * NULL.  Writes gx [N, in1], gy [E, in2], gw [E, weight_numel] and, when env
  * is given and genv is not NULL, genv [E].  Any of gx/gy/gw may be NULL to skip
- * it.  workspace must hold luna_uvu_conv_bwd_workspace bytes.
+ * it.  A destination-owned kernel streams each node's in-edges (dst CSR:
+ * src, dst_rowptr, node_order) and writes gw, gy partials and one gx message
+ * per edge into the workspace; a second pass sums the messages over each
+ * node's out-edges (src CSR: src_rowptr, edge_ids_by_src).  workspace must hold
+ * luna_uvu_conv_bwd_workspace bytes.
  * replaces: run_uvu_conv_bwd (src/lunatp/uvu_conv/kernels/backward.py:505-512)
  */
 int luna_uvu_conv_bwd(const LunaUvuPlan* plan,
                       const void* x, const void* y, const void* w, const void* env,
                       const void* g, const void* gl0,
-                      const int32_t* dst, const int32_t* src_rowptr,
-                      const int32_t* edge_ids_by_src,
-                      const int32_t* source_node_order,
+                      const int32_t* src, const int32_t* dst_rowptr,
+                      const int32_t* node_order,
+                      const int32_t* src_rowptr, const int32_t* edge_ids_by_src,
                       void* gx, void* gy, void* gw, void* genv,
                       void* workspace, size_t workspace_bytes,
                       int64_t num_nodes, int64_t num_edges, LunaStream stream);
+
+/*
+ * Measurement hook (no counterpart in the reference): while enabled, every
+ * launch is bracketed by HIP events on its stream.  luna_profile_collect waits
+ * for the recorded events and writes one line per kernel name,
+ * "<name> <launches> <total_ms> <min_ms> <max_ms>", then clears the records.
+ */
+int luna_profile_enable(int on);
+int luna_profile_collect(char* buffer, size_t capacity, size_t* needed);
 
 #ifdef __cplusplus
 }

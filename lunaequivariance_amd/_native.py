@@ -35,8 +35,11 @@ PROTOTYPES = {
     "luna_uvu_plan_precompile": (ctypes.c_int, [_VP]),
     "luna_uvu_conv_fwd": (ctypes.c_int, [_VP] + [_VP] * 4 + [_I32P] * 3 + [_VP, _VP, _I64, _I64, _VP]),
     "luna_uvu_conv_bwd_workspace": (ctypes.c_int, [_VP, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
-    "luna_uvu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 4 + [_VP] * 5
+    "luna_uvu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 5 + [_VP] * 5
                           + [ctypes.c_size_t, _I64, _I64, _VP]),
+    "luna_profile_enable": (ctypes.c_int, [ctypes.c_int]),
+    "luna_profile_collect": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t,
+                                             ctypes.POINTER(ctypes.c_size_t)]),
 }
 
 _lib = None
@@ -67,6 +70,22 @@ def check(status: int, what: str) -> None:
     if status != 0:
         message = lib().luna_last_error().decode(errors="replace")
         raise RuntimeError(f"{what}: {message}")
+
+
+def profile_enable(on: bool) -> None:
+    check(lib().luna_profile_enable(1 if on else 0), "luna_profile_enable")
+
+
+def profile_collect() -> dict:
+    """{kernel name: (launches, total_ms, min_ms, max_ms)} since the last collect."""
+    buffer = ctypes.create_string_buffer(1 << 16)
+    needed = ctypes.c_size_t()
+    check(lib().luna_profile_collect(buffer, len(buffer), ctypes.byref(needed)), "luna_profile_collect")
+    result = {}
+    for line in buffer.value.decode().splitlines():
+        name, count, total, low, high = line.split()
+        result[name] = (int(count), float(total), float(low), float(high))
+    return result
 
 
 def cache_dir() -> str:

@@ -15,7 +15,7 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 SOURCES = ["uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp"]
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O2", "-fPIC", "-shared", "-std=c++17",
+    "--offload-arch=gfx950", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wno-format-security",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

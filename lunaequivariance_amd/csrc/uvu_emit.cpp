@@ -4,19 +4,24 @@
 // a wave holds all partial products and output accumulators of its group in
 // VGPRs while edge attributes and graph indices, which are uniform across the
 // wave, come through scalar loads.  One lane owns one channel u of a
-// 64-channel chunk.
+// 64-channel chunk.  Edge loops are software-pipelined: the gathered source
+// row and the weight row of edge e+1 are in flight while edge e is computed.
 //
 // Forward (dst-owned, as the reference's ordered forward kernel,
 // src/lunatp/uvu_conv/kernels/forward.py:398-427):
 //   out[t, ob + u*d3 + k] = sum_{e in row t} env[e] * w[e, wo + u*ws]
 //                           * sum_{(i,j,k)} c_ijk x[src[e], xb + u*d1 + i] y[e, yb + j]
-// Backward (src-owned, as src/lunatp/uvu_conv/kernels/backward.py:183-333):
-//   q_ij = sum_k c_ijk G_k with G = env[e] * g[dst[e]] (+ gl0 for scalar paths)
+// Backward (the math of src/lunatp/uvu_conv/kernels/backward.py:183-333, but
+// destination-owned so the wide output seed g[t] is read once per node):
+//   q_ij = sum_k c_ijk G_k with G = env[e] * g[t] (+ gl0 for scalar paths)
 //   gw[e, wo + u*ws] = sum_ij x_i y_j q_ij
-//   gx[s, xb + u*d1 + i] = sum_e w sum_j y_j q_ij
+//   msg[e, xb + u*d1 + i] = w sum_j y_j q_ij;  gx[s] = sum_{e: src[e]=s} msg[e]
 //   gy[e, yb + j] = sum_u w sum_i x_i q_ij      (partials per wave, then reduced)
 //   genv[e] = sum_u sum_k w g_k t_k, t_k = sum c x_i y_j
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <set>
 #include <sstream>
@@ -30,13 +35,38 @@ namespace {
 struct Code {
   std::ostringstream s;
   template <typename... A>
-  void line(const char* fmt, A... args) {
+  __attribute__((format(printf, 2, 0))) void line(const char* fmt, A... args) {
     char buffer[1024];
     std::snprintf(buffer, sizeof(buffer), fmt, args...);
     s << buffer << '\n';
   }
   void raw(const std::string& text) { s << text; }
 };
+
+// Emission switches, overridable through LUNAEQ_AMD_EMIT="prefetch=0,hoist=1,fwpe=2,bwpe=2".
+struct Options {
+  bool prefetch = true;  // software-pipeline the edge loops
+  bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
+  int fwd_wpe = 0;       // amdgpu_waves_per_eu hint for the forward (0 = none)
+  int bwd_wpe = 0;       // same for the backward
+};
+
+Options options() {
+  Options o;
+  const char* text = std::getenv("LUNAEQ_AMD_EMIT");
+  if (!text) return o;
+  std::string s(text);
+  auto value = [&](const char* key, int fallback) {
+    std::string k = std::string(key) + "=";
+    size_t at = s.find(k);
+    return at == std::string::npos ? fallback : std::atoi(s.c_str() + at + k.size());
+  };
+  o.prefetch = value("prefetch", o.prefetch) != 0;
+  o.hoist = value("hoist", o.hoist) != 0;
+  o.fwd_wpe = value("fwpe", o.fwd_wpe);
+  o.bwd_wpe = value("bwpe", o.bwd_wpe);
+  return o;
+}
 
 std::string literal(double c, int bits) {
   char buffer[64];
@@ -59,11 +89,22 @@ std::string prelude(const Spec& spec) {
   s << "#define OUTD " << spec.out << "LL\n";
   s << "#define WNUM " << spec.wnum << "LL\n";
   s << "#define L0DIM " << spec.l0_dim << "LL\n";
+  s << "#define PART_W " << spec.in2 + 1 << "LL\n";
+  // Lane exchange v[lane ^ M]: DPP quad permutes for M = 1, 2, a swizzle for
+  // M = 4..16 (within 32 lanes) and a permute through LDS hardware for M = 32.
   s << R"(
-__device__ __forceinline__ real wave_sum(real v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+template <int M>
+__device__ __forceinline__ int xchg_bits(int v) {
+  if constexpr (M == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
+  else if constexpr (M == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
+  else if constexpr (M < 32) return __builtin_amdgcn_ds_swizzle(v, 0x1F | (M << 10));
+  else return __builtin_amdgcn_ds_bpermute((int)((threadIdx.x ^ 32u) << 2), v);
+}
+template <int M>
+__device__ __forceinline__ float xchg(float v) { return __int_as_float(xchg_bits<M>(__float_as_int(v))); }
+template <int M>
+__device__ __forceinline__ double xchg(double v) {
+  return __hiloint2double(xchg_bits<M>(__double2hiint(v)), xchg_bits<M>(__double2loint(v)));
 }
 )";
   return s.str();
@@ -87,37 +128,116 @@ GroupUse group_use(const Spec& spec, const Group& g) {
   return use;
 }
 
-void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, bool l0) {
+// Reduce-scatter of `names` over the 64 lanes: log2(P) halving steps leave
+// every lane with one value index summed over a subset of lanes, then full
+// exchanges finish the sum.  Lane L then holds value index L >> shift, and
+// the lanes with (L & low_mask) == 0 write it.
+std::string emit_butterfly(Code& c, std::vector<std::string> names, const char* prefix, int* shift,
+                           int* low_mask) {
+  int count = 1;
+  while (count < (int)names.size()) count *= 2;
+  while ((int)names.size() < count) names.push_back("(real)0");
+  int level = 0, split_bits = 0;
+  for (int m = 32; m >= 1; m >>= 1, ++level) {
+    if (count == 1) {
+      c.line("        %s = %s + xchg<%d>(%s);", names[0].c_str(), names[0].c_str(), m, names[0].c_str());
+      continue;
+    }
+    const int half = count / 2;
+    c.line("        const bool %sh%d = (lane & %d) != 0;", prefix, level, m);
+    std::vector<std::string> next;
+    for (int n = 0; n < half; ++n) {
+      std::string name = std::string(prefix) + std::to_string(level) + "_" + std::to_string(n);
+      c.line("        real %s = (%sh%d ? %s : %s) + xchg<%d>(%sh%d ? %s : %s);", name.c_str(), prefix, level,
+             names[half + n].c_str(), names[n].c_str(), m, prefix, level, names[n].c_str(),
+             names[half + n].c_str());
+      next.push_back(name);
+    }
+    names = next;
+    count = half;
+    ++split_bits;
+  }
+  *shift = 6 - split_bits;
+  *low_mask = (1 << (6 - split_bits)) - 1;
+  return names[0];
+}
+
+void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, bool l0, const Options& opt) {
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
+  const int np = (int)g.paths.size();
   c.line("    const int u = (slot - %d) * 64 + lane;", g.slot_base);
   c.line("    const bool active = u < %d;", g.channels);
   c.line("    const int uc = active ? u : %d;", g.channels - 1);
   for (size_t b = 0; b < g.blocks.size(); ++b)
     for (int k = 0; k < g.blocks[b].d3; ++k) c.line("    real A%zu_%d = 0;", b, k);
-  c.line("    for (int e = beg; e < end; ++e) {");
-  c.line("      const int s = src[e];");
-  c.line("      const real* xr = x + (i64)s * IN1 + (%d + uc * %d);", g.x_off, g.d1);
-  for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = xr[%d];", i, i);
+  // Edge operands: the gathered x block (d1 values) and one weight per path.
+  auto load_edge = [&](const char* edge, const char* srcv) {
+    c.line("      {");
+    c.line("        const real* xq = x + (i64)%s * IN1 + (%d + uc * %d);", srcv, g.x_off, g.d1);
+    for (int i = 0; i < g.d1; ++i) c.line("        nx%d = xq[%d];", i, i);
+    c.line("        const real* wq = w + (i64)%s * WNUM;", edge);
+    for (int n = 0; n < np; ++n) {
+      const Path& q = spec.paths[g.paths[n]];
+      c.line("        nw%d = wq[%d + uc * %d];", n, q.w_off, q.w_stride);
+    }
+    c.line("      }");
+  };
+  if (opt.prefetch) {
+    c.line("    if (beg < end) {");
+    for (int i = 0; i < g.d1; ++i) c.line("      real nx%d;", i);
+    for (int n = 0; n < np; ++n) c.line("      real nw%d;", n);
+    c.line("      int sn = src[beg];");
+    load_edge("beg", "sn");
+    c.line("      for (int e = beg; e < end; ++e) {");
+    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = nx%d;", i, i);
+    for (int n = 0; n < np; ++n) c.line("      const real w%d = nw%d;", n, n);
+    c.line("      const int en = e + 1 < end ? e + 1 : e;");
+    c.line("      sn = src[en];");
+    load_edge("en", "sn");
+  } else {
+    c.line("    {");
+    c.line("      for (int e = beg; e < end; ++e) {");
+    c.line("      const int s = src[e];");
+    c.line("      const real* xr = x + (i64)s * IN1 + (%d + uc * %d);", g.x_off, g.d1);
+    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = xr[%d];", i, i);
+    c.line("      const real* wr = w + (i64)e * WNUM;");
+    for (int n = 0; n < np; ++n) {
+      const Path& q = spec.paths[g.paths[n]];
+      c.line("      const real w%d = wr[%d + uc * %d];", n, q.w_off, q.w_stride);
+    }
+  }
   c.line("      const real* yr = y + (i64)e * IN2;");
   for (int yi : use.ys) c.line("      const real y%d = yr[%d];", yi, yi);
-  c.line("      const real* wr = w + (i64)e * WNUM;");
   if (env) c.line("      const real ev = env[e];");
-  for (const auto& pr : use.products)
-    c.line("      const real p%d_%d = x%d * y%d;", pr.first, pr.second, pr.first, pr.second);
   // l0 columns are summed over the paths (edge copies) sharing them.
   std::map<int, std::vector<int>> l0_cols;
-  for (size_t n = 0; n < g.paths.size(); ++n) {
+  for (int n = 0; n < np; ++n) {
     const Path& q = spec.paths[g.paths[n]];
-    if (l0 && q.l0_col >= 0) l0_cols[q.l0_col].push_back((int)n);
+    if (l0 && q.l0_col >= 0) l0_cols[q.l0_col].push_back(n);
   }
   for (const auto& col : l0_cols) c.line("      real L%d = 0;", col.first);
-  for (size_t n = 0; n < g.paths.size(); ++n) {
+  // Paths in edge-block order; each x*y product is formed just before the
+  // first path that needs it, which bounds the products alive at once.
+  std::vector<int> order(np);
+  for (int n = 0; n < np; ++n) order[n] = n;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+    return spec.paths[g.paths[a]].y_off < spec.paths[g.paths[b]].y_off;
+  });
+  std::set<std::pair<int, int>> formed;
+  for (int n : order) {
     const Path& q = spec.paths[g.paths[n]];
     const int b = g.path_block[n];
+    for (const Term& t : q.terms) {
+      auto key = std::make_pair(t.i, q.y_off + t.j);
+      if (formed.insert(key).second)
+        c.line("      const real p%d_%d = x%d * y%d;", key.first, key.second, key.first, key.second);
+    }
     c.line("      {");
-    c.line("        const real wraw = wr[%d + uc * %d];", q.w_off, q.w_stride);
-    c.line("        const real wv = %s;", env ? "wraw * ev" : "wraw");
+    if (env)
+      c.line("        const real wv = w%d * ev;", n);
+    else
+      c.line("        const real wv = w%d;", n);
     std::map<int, std::vector<const Term*>> by_k;
     for (const Term& t : q.terms) by_k[t.k].push_back(&t);
     for (const auto& kv : by_k) {
@@ -134,14 +254,12 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
       }
       c.line("        A%d_%d = FMA(wv, t%d, A%d_%d);", b, k, k, b, k);
     }
-    if (l0 && q.l0_col >= 0) {
-      if (by_k.count(0))
-        c.line("        L%d = FMA(wraw, t0, L%d);", q.l0_col, q.l0_col);
-    }
+    if (l0 && q.l0_col >= 0 && by_k.count(0)) c.line("        L%d = FMA(w%d, t0, L%d);", q.l0_col, n, q.l0_col);
     c.line("      }");
   }
   for (const auto& col : l0_cols)
-    c.line("      if (l0 && active) l0[(i64)e * L0DIM + %d + u] = L%d;", col.first, col.first);
+    c.line("      l0[(i64)e * L0DIM + %d + uc] = L%d;", col.first, col.first);
+  c.line("      }");
   c.line("    }");
   c.line("    if (active) {");
   for (size_t b = 0; b < g.blocks.size(); ++b) {
@@ -157,46 +275,81 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
   c.line("    }");
 }
 
-void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bool gl0) {
+// Backward, destination-owned: the wave keeps the output seeds g[t] of its
+// group in registers and streams the node's in-edges, writing gw and the gy
+// partials per edge and the per-edge gx message msg[e, x block]; a second
+// kernel sums the messages over each source node's out-edges.
+void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
+                         bool want_msg, bool want_part, const Options& opt) {
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
-  const int pw = spec.in2 + (env ? 1 : 0);
+  const int np = (int)g.paths.size();
   c.line("    const int u = (slot - %d) * 64 + lane;", g.slot_base);
   c.line("    const bool active = u < %d;", g.channels);
   c.line("    const int uc = active ? u : %d;", g.channels - 1);
-  c.line("    const real* xr = x + (i64)s * IN1 + (%d + uc * %d);", g.x_off, g.d1);
-  for (int i = 0; i < g.d1; ++i) c.line("    const real x%d = xr[%d];", i, i);
-  for (int i = 0; i < g.d1; ++i) c.line("    real GX%d = 0;", i);
-  c.line("    for (int pos = beg; pos < end; ++pos) {");
-  c.line("      const int e = ebs[pos];");
-  c.line("      const int d = dst[e];");
-  c.line("      const real* yr = y + (i64)e * IN2;");
-  for (int yi : use.ys) c.line("      const real y%d = yr[%d];", yi, yi);
-  c.line("      const real* wr = w + (i64)e * WNUM;");
-  if (env) c.line("      const real ev = env[e];");
+  std::vector<std::string> seeds;
   for (size_t b = 0; b < g.blocks.size(); ++b) {
     const AccBlock& blk = g.blocks[b];
-    c.line("      const real* g%zu = g + (i64)d * OUTD + (%d + uc * %d);", b, blk.out_off, blk.d3);
+    c.line("    const real* g%zu = g + (i64)t * OUTD + (%d + uc * %d);", b, blk.out_off, blk.d3);
     for (int k = 0; k < blk.d3; ++k) {
-      c.line("      const real G%zu_%d = g%zu[%d];", b, k, b, k);
-      c.line("      const real H%zu_%d = %s;", b, k, env ? ("ev * G" + std::to_string(b) + "_" + std::to_string(k)).c_str()
-                                                       : ("G" + std::to_string(b) + "_" + std::to_string(k)).c_str());
+      c.line("    real G%zu_%d = g%zu[%d];", b, k, b, k);
+      seeds.push_back("G" + std::to_string(b) + "_" + std::to_string(k));
     }
   }
-  for (int yi : use.ys) c.line("      real GY%d = 0;", yi);
-  if (env) {
-    c.line("      real GE = 0;");
-    for (const auto& pr : use.products)
-      c.line("      const real p%d_%d = x%d * y%d;", pr.first, pr.second, pr.first, pr.second);
+  auto load_edge = [&](const char* edge, const char* srcv) {
+    c.line("      {");
+    c.line("        const real* xq = x + (i64)%s * IN1 + (%d + uc * %d);", srcv, g.x_off, g.d1);
+    for (int i = 0; i < g.d1; ++i) c.line("        nx%d = xq[%d];", i, i);
+    c.line("        const real* wq = w + (i64)%s * WNUM;", edge);
+    for (int n = 0; n < np; ++n) {
+      const Path& q = spec.paths[g.paths[n]];
+      c.line("        nw%d = wq[%d + uc * %d];", n, q.w_off, q.w_stride);
+    }
+    c.line("      }");
+  };
+  if (opt.prefetch) {
+    c.line("    if (beg < end) {");
+    for (int i = 0; i < g.d1; ++i) c.line("      real nx%d;", i);
+    for (int n = 0; n < np; ++n) c.line("      real nw%d;", n);
+    c.line("      int sn = src[beg];");
+    load_edge("beg", "sn");
+    c.line("      for (int e = beg; e < end; ++e) {");
+    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = nx%d;", i, i);
+    for (int n = 0; n < np; ++n) c.line("      const real w%d = nw%d;", n, n);
+    c.line("      const int en = e + 1 < end ? e + 1 : e;");
+    c.line("      sn = src[en];");
+    load_edge("en", "sn");
+  } else {
+    c.line("    {");
+    c.line("      for (int e = beg; e < end; ++e) {");
+    c.line("      const int s = src[e];");
+    c.line("      const real* xr = x + (i64)s * IN1 + (%d + uc * %d);", g.x_off, g.d1);
+    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = xr[%d];", i, i);
+    c.line("      const real* wr = w + (i64)e * WNUM;");
+    for (int n = 0; n < np; ++n) {
+      const Path& q = spec.paths[g.paths[n]];
+      c.line("      const real w%d = wr[%d + uc * %d];", n, q.w_off, q.w_stride);
+    }
   }
-  for (size_t n = 0; n < g.paths.size(); ++n) {
+  if (!opt.hoist) {
+    // Opaque to the optimiser: keeps the edge-invariant q_ij inside the loop
+    // instead of holding all of them in registers across it.
+    for (const auto& name : seeds) c.line("      asm volatile(\"\" : \"+v\"(%s));", name.c_str());
+  }
+  c.line("      const real* yr = y + (i64)e * IN2;");
+  for (int yi : use.ys) c.line("      const real y%d = yr[%d];", yi, yi);
+  if (env) c.line("      const real ev = env[e];");
+  for (int i = 0; i < g.d1; ++i) c.line("      real M%d = 0;", i);
+  for (int yi : use.ys) c.line("      real GY%d = 0;", yi);
+  if (env) c.line("      real GE = 0;");
+  for (int n = 0; n < np; ++n) {
     const Path& q = spec.paths[g.paths[n]];
     const int b = g.path_block[n];
-    c.line("      {");
-    c.line("        const real wv = active ? wr[%d + uc * %d] : (real)0;", q.w_off, q.w_stride);
     const bool scalar_seed = gl0 && q.l0_col >= 0;
-    if (scalar_seed) c.line("        const real S0 = H%d_0 + gl0[(i64)e * L0DIM + %d + uc];", b, q.l0_col);
-    // q_ij for every (i, j) pair of the path.
+    c.line("      {");
+    c.line("        const real wv = w%d;", n);
+    if (scalar_seed) c.line("        const real S0 = %sG%d_0 + gl0[(i64)e * L0DIM + %d + uc];",
+                            env ? "ev * " : "", b, q.l0_col);
     std::map<std::pair<int, int>, std::vector<const Term*>> by_ij;
     for (const Term& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
     std::set<int> is, js;
@@ -211,8 +364,7 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
       bool first = true;
       for (const Term* t : kv.second) {
         std::string coef = literal(t->c, bits);
-        std::string seed = (scalar_seed && t->k == 0) ? std::string("S0")
-                                                      : "H" + std::to_string(b) + "_" + std::to_string(t->k);
+        std::string seed = scalar_seed ? std::string("S0") : "G" + std::to_string(b) + "_" + std::to_string(t->k);
         if (first) {
           c.line("        real q%d_%d = %s * %s;", i, j, coef.c_str(), seed.c_str());
           first = false;
@@ -223,73 +375,95 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
       c.line("        b%d = FMA(x%d, q%d_%d, b%d);", j, i, i, j, j);
       c.line("        a%d = FMA(y%d, q%d_%d, a%d);", i, q.y_off + j, i, j, i);
     }
-    // gw = sum_j y_j b_j
+    // gw = sum_i x_i a_i  (= sum_ij x_i y_j q_ij)
     bool first = true;
-    for (int j : js) {
+    for (int i : is) {
       if (first) {
-        c.line("        real gwv = y%d * b%d;", q.y_off + j, j);
+        c.line("        real gwv = x%d * a%d;", i, i);
         first = false;
       } else {
-        c.line("        gwv = FMA(y%d, b%d, gwv);", q.y_off + j, j);
+        c.line("        gwv = FMA(x%d, a%d, gwv);", i, i);
       }
     }
     if (first) c.line("        real gwv = 0;");
-    c.line("        if (gw && active) gw[(i64)e * WNUM + %d + u * %d] = gwv;", q.w_off, q.w_stride);
-    for (int j : js) c.line("        GY%d = FMA(wv, b%d, GY%d);", q.y_off + j, j, q.y_off + j);
-    for (int i : is) c.line("        GX%d = FMA(wv, a%d, GX%d);", i, i, i);
+    const bool fold_env = env && !scalar_seed;
     if (env) {
-      // genv: sum_k g_k t_k with t_k = sum c x_i y_j (raw output seed, no gl0).
-      std::map<int, std::vector<const Term*>> by_k;
-      for (const Term& t : q.terms) by_k[t.k].push_back(&t);
-      c.line("        real tg = 0;");
-      for (const auto& kv : by_k) {
-        const int k = kv.first;
+      if (scalar_seed) {
+        // genv needs sum_k g_k t_k with the raw node seed: t_0 = sum c x_i y_j.
         bool f2 = true;
-        for (const Term* t : kv.second) {
-          std::string coef = literal(t->c, bits);
+        for (const Term& t : q.terms) {
+          std::string coef = literal(t.c, bits);
           if (f2) {
-            c.line("        real t%d = %s * p%d_%d;", k, coef.c_str(), t->i, q.y_off + t->j);
+            c.line("        real t0 = %s * (x%d * y%d);", coef.c_str(), t.i, q.y_off + t.j);
             f2 = false;
           } else {
-            c.line("        t%d = FMA(%s, p%d_%d, t%d);", k, coef.c_str(), t->i, q.y_off + t->j, k);
+            c.line("        t0 = FMA(%s, x%d * y%d, t0);", coef.c_str(), t.i, q.y_off + t.j);
           }
         }
-        c.line("        tg = FMA(G%d_%d, t%d, tg);", b, k, k);
+        if (f2) c.line("        real t0 = 0;");
+        c.line("        GE = FMA(wv, G%d_0 * t0, GE);", b);
+      } else {
+        c.line("        GE = FMA(wv, gwv, GE);");
       }
-      c.line("        GE = FMA(wv, tg, GE);");
+    }
+    if (fold_env) {
+      c.line("        gwv *= ev;");
+      c.line("        const real ws = wv * ev;");
+    } else {
+      c.line("        const real ws = wv;");
+    }
+    if (want_gw) c.line("        gw[(i64)e * WNUM + %d + uc * %d] = gwv;", q.w_off, q.w_stride);
+    for (int j : js) c.line("        GY%d = FMA(ws, b%d, GY%d);", q.y_off + j, j, q.y_off + j);
+    for (int i : is) c.line("        M%d = FMA(ws, a%d, M%d);", i, i, i);
+    c.line("      }");
+  }
+  if (want_msg) {
+    // Lanes past the last channel repeat channel C-1 exactly, so their stores
+    // write identical values; only the cross-lane sums below must mask them.
+    c.line("      {");
+    c.line("        real* mr = msg + (i64)e * IN1 + (%d + uc * %d);", g.x_off, g.d1);
+    for (int i = 0; i < g.d1; ++i) {
+      if (g.gx_accumulate)
+        c.line("        mr[%d] += M%d;", i, i);
+      else
+        c.line("        mr[%d] = M%d;", i, i);
     }
     c.line("      }");
   }
-  // Reduce the edge-attribute partials over the wave's channels.
-  c.line("      real* pr = part + ((i64)(%d + (slot - %d)) * E + e) * %d;", g.gy_slot_base, g.slot_base, pw);
-  for (int yi : use.ys) {
-    c.line("      GY%d = wave_sum(GY%d);", yi, yi);
-    c.line("      if (lane == 0 && part) pr[%d] = GY%d;", yi, yi);
+  // gy (and genv) partials of this wave: reduce over the 64 channels.
+  std::vector<std::string> values;
+  for (int yi : use.ys) values.push_back("GY" + std::to_string(yi));
+  if (env) values.push_back("GE");
+  if (want_part && !values.empty()) {
+    c.line("      {");
+    for (const auto& v : values) c.line("        %s = active ? %s : (real)0;", v.c_str(), v.c_str());
+    int shift = 0, low = 0;
+    std::string total = emit_butterfly(c, values, "r", &shift, &low);
+    c.line("        const int col = lane >> %d;", shift);
+    c.line("        if ((lane & %d) == 0 && col < %zu)", low, values.size());
+    c.line("          part[((i64)(%d + (slot - %d)) * E + e) * PART_W + col] = %s;", g.gy_slot_base, g.slot_base,
+           total.c_str());
+    c.line("      }");
   }
-  if (env) {
-    c.line("      GE = wave_sum(GE);");
-    c.line("      if (lane == 0 && part) pr[%d] = GE;", spec.in2);
-  }
+  c.line("      }");
   c.line("    }");
-  c.line("    if (gx && active) {");
-  c.line("      real* gxr = gx + (i64)s * IN1 + (%d + u * %d);", g.x_off, g.d1);
-  for (int i = 0; i < g.d1; ++i) {
-    if (g.gx_accumulate)
-      c.line("      gxr[%d] += GX%d;", i, i);
-    else
-      c.line("      gxr[%d] = GX%d;", i, i);
-  }
-  c.line("    }");
+}
+
+std::string kernel_attributes(int wpe) {
+  if (wpe <= 0) return "";
+  return "__attribute__((amdgpu_waves_per_eu(" + std::to_string(wpe) + "))) ";
 }
 
 }  // namespace
 
 std::string emit_forward(const Plan& plan, bool env, bool l0) {
   const Spec& spec = plan.spec;
+  const Options opt = options();
   Code c;
   c.raw(prelude(spec));
   for (int phase = 0; phase < plan.fwd_phases; ++phase) {
-    c.line("extern \"C\" __global__ void __launch_bounds__(64) luna_uvu_fwd_p%d(", phase);
+    c.line("extern \"C\" __global__ void __launch_bounds__(64) %sluna_uvu_fwd_p%d(",
+           kernel_attributes(opt.fwd_wpe).c_str(), phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
     c.line("    const real* __restrict__ env, const int* __restrict__ src, const int* __restrict__ rowptr,");
     c.line("    const int* __restrict__ order, real* __restrict__ out, real* __restrict__ l0) {");
@@ -303,7 +477,7 @@ std::string emit_forward(const Plan& plan, bool env, bool l0) {
       if (g.phase != phase) continue;
       c.line("  %sif (slot < %d) {", first ? "" : "else ", g.slot_base + g.chunks);
       first = false;
-      emit_forward_group(c, spec, g, env, l0);
+      emit_forward_group(c, spec, g, env, l0, opt);
       c.line("  }");
     }
     c.line("}");
@@ -311,55 +485,63 @@ std::string emit_forward(const Plan& plan, bool env, bool l0) {
   return c.s.str();
 }
 
-std::string emit_backward(const Plan& plan, bool env, bool gl0) {
+std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bool want_msg, bool want_part) {
   const Spec& spec = plan.spec;
-  const int pw = spec.in2 + (env ? 1 : 0);
+  const Options opt = options();
   Code c;
   c.raw(prelude(spec));
   for (int phase = 0; phase < plan.bwd_phases; ++phase) {
-    c.line("extern \"C\" __global__ void __launch_bounds__(64) luna_uvu_bwd_p%d(", phase);
+    c.line("extern \"C\" __global__ void __launch_bounds__(64) %sluna_uvu_bwd_p%d(",
+           kernel_attributes(opt.bwd_wpe).c_str(), phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
     c.line("    const real* __restrict__ env, const real* __restrict__ g, const real* __restrict__ gl0,");
-    c.line("    const int* __restrict__ dst, const int* __restrict__ srow, const int* __restrict__ ebs,");
-    c.line("    const int* __restrict__ sorder, real* __restrict__ gx, real* __restrict__ gw,");
-    c.line("    real* __restrict__ part, i64 E) {");
+    c.line("    const int* __restrict__ src, const int* __restrict__ rowptr, const int* __restrict__ order,");
+    c.line("    real* __restrict__ gw, real* __restrict__ msg, real* __restrict__ part, i64 E) {");
     c.line("  const int lane = threadIdx.x;");
-    c.line("  const int s = sorder[blockIdx.x];");
-    c.line("  const int beg = srow[s];");
-    c.line("  const int end = srow[s + 1];");
+    c.line("  const int t = order[blockIdx.x];");
+    c.line("  const int beg = rowptr[t];");
+    c.line("  const int end = rowptr[t + 1];");
     c.line("  const int slot = blockIdx.y;");
     bool first = true;
     for (const Group& g : plan.bwd_groups) {
       if (g.phase != phase) continue;
       c.line("  %sif (slot < %d) {", first ? "" : "else ", g.slot_base + g.chunks);
       first = false;
-      emit_backward_group(c, spec, g, env, gl0);
+      emit_backward_group(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt);
       c.line("  }");
     }
     c.line("}");
   }
   // Reduction of the per-wave partials into gy (and genv).  Table: for each
-  // partial column, the slots that wrote it.
-  std::vector<std::vector<int>> writers(pw);
+  // output column, the (slot, partial column) pairs that hold a share of it.
+  const int pw = spec.in2 + (env ? 1 : 0);
+  std::vector<std::vector<std::pair<int, int>>> writers(pw);
   for (const Group& g : plan.bwd_groups) {
     GroupUse use = group_use(spec, g);
     for (int chunk = 0; chunk < g.chunks; ++chunk) {
-      for (int yi : use.ys) writers[yi].push_back(g.gy_slot_base + chunk);
-      if (env) writers[spec.in2].push_back(g.gy_slot_base + chunk);
+      int col = 0;
+      for (int yi : use.ys) writers[yi].push_back({g.gy_slot_base + chunk, col++});
+      if (env) writers[spec.in2].push_back({g.gy_slot_base + chunk, col});
     }
   }
-  std::vector<int> begin(pw + 1, 0), ids;
+  std::vector<int> begin(pw + 1, 0), slots, cols;
   for (int col = 0; col < pw; ++col) {
-    begin[col] = (int)ids.size();
-    for (int s : writers[col]) ids.push_back(s);
+    begin[col] = (int)slots.size();
+    for (const auto& sc : writers[col]) {
+      slots.push_back(sc.first);
+      cols.push_back(sc.second);
+    }
   }
-  begin[pw] = (int)ids.size();
-  c.s << "__constant__ int reduce_begin[" << pw + 1 << "] = {";
-  for (int v : begin) c.s << v << ",";
-  c.s << "};\n__constant__ int reduce_slot[" << (ids.empty() ? 1 : ids.size()) << "] = {";
-  for (int v : ids) c.s << v << ",";
-  if (ids.empty()) c.s << "0";
-  c.s << "};\n";
+  begin[pw] = (int)slots.size();
+  auto table = [&](const char* name, const std::vector<int>& values) {
+    c.s << "__constant__ int " << name << "[" << std::max<size_t>(values.size(), 1) << "] = {";
+    for (int v : values) c.s << v << ",";
+    if (values.empty()) c.s << "0";
+    c.s << "};\n";
+  };
+  table("reduce_begin", begin);
+  table("reduce_slot", slots);
+  table("reduce_col", cols);
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_bwd_reduce(");
   c.line("    const real* __restrict__ part, real* __restrict__ gy, real* __restrict__ genv, i64 E) {");
   c.line("  const i64 idx = (i64)blockIdx.x * 256 + threadIdx.x;");
@@ -368,9 +550,46 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0) {
   c.line("  const int col = (int)(idx - e * %d);", pw);
   c.line("  real acc = 0;");
   c.line("  for (int n = reduce_begin[col]; n < reduce_begin[col + 1]; ++n)");
-  c.line("    acc += part[(i64)reduce_slot[n] * E * %d + idx];", pw);
+  c.line("    acc += part[((i64)reduce_slot[n] * E + e) * PART_W + reduce_col[n]];");
   c.line("  if (col < %d) { if (gy) gy[e * IN2 + col] = acc; }", spec.in2);
   if (env) c.line("  else if (genv) genv[e] = acc;");
+  c.line("}");
+  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_fill(real* __restrict__ p, i64 n) {");
+  c.line("  const i64 i = (i64)blockIdx.x * 256 + threadIdx.x;");
+  c.line("  if (i < n) p[i] = 0;");
+  c.line("}");
+  // Segment sum of the gx messages over each source node's out-edges.
+  std::vector<std::pair<long, long>> ranges;
+  for (const Group& g : plan.bwd_groups) ranges.push_back({g.x_off, g.x_off + (long)g.channels * g.d1});
+  std::sort(ranges.begin(), ranges.end());
+  std::vector<std::pair<long, long>> merged;
+  for (const auto& r : ranges) {
+    if (!merged.empty() && r.first <= merged.back().second)
+      merged.back().second = std::max(merged.back().second, r.second);
+    else
+      merged.push_back(r);
+  }
+  c.line("__device__ __forceinline__ bool covered(int col) {");
+  if (merged.size() == 1 && merged[0].first == 0 && merged[0].second == spec.in1) {
+    c.line("  return true;");
+  } else {
+    c.raw("  return false");
+    for (const auto& r : merged) c.s << " || (col >= " << r.first << " && col < " << r.second << ")";
+    c.raw(";\n");
+  }
+  c.line("}");
+  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_bwd_gather(");
+  c.line("    const real* __restrict__ msg, const int* __restrict__ srow, const int* __restrict__ ebs,");
+  c.line("    real* __restrict__ gx) {");
+  c.line("  const int s = blockIdx.x;");
+  c.line("  const int col = blockIdx.y * 256 + threadIdx.x;");
+  c.line("  if (col >= IN1) return;");
+  c.line("  real acc = 0;");
+  c.line("  if (covered(col)) {");
+  c.line("    const int beg = srow[s], end = srow[s + 1];");
+  c.line("    for (int p = beg; p < end; ++p) acc += msg[(i64)ebs[p] * IN1 + col];");
+  c.line("  }");
+  c.line("  gx[(i64)s * IN1 + col] = acc;");
   c.line("}");
   return c.s.str();
 }

@@ -75,7 +75,7 @@ void build_schedule(Plan& plan);
 
 // Emitted HIP source of one kernel module variant.
 std::string emit_forward(const Plan& plan, bool env, bool l0);
-std::string emit_backward(const Plan& plan, bool env, bool gl0);
+std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bool want_msg, bool want_part);
 
 // Compile HIP source for gfx950 with hipRTC, through the on-disk cache.
 std::vector<char> compile_hip(const std::string& source, const std::string& cache_dir,

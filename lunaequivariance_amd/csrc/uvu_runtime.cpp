@@ -6,6 +6,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -103,10 +104,10 @@ std::vector<char> compile_hip(const std::string& source, const std::string& cach
 namespace {
 
 std::string source_for(const Plan& plan, const std::string& variant) {
-  // Variant names: fwd<env><l0> and bwd<env><gl0>, each flag '0' or '1'.
-  const bool a = variant[3] == '1', b = variant[4] == '1';
-  if (variant.compare(0, 3, "fwd") == 0) return emit_forward(plan, a, b);
-  return emit_backward(plan, a, b);
+  // Variant names: fwd<env><l0> and bwd<env><gl0><gw><msg><part>, each flag '0' or '1'.
+  auto flag = [&](size_t i) { return variant.size() > i && variant[i] == '1'; };
+  if (variant.compare(0, 3, "fwd") == 0) return emit_forward(plan, flag(3), flag(4));
+  return emit_backward(plan, flag(3), flag(4), flag(5), flag(6), flag(7));
 }
 
 const std::vector<char>& code_for(Plan& plan, const std::string& variant) {
@@ -137,11 +138,37 @@ hipFunction_t function_for(hipModule_t module, const std::string& name) {
   return function;
 }
 
-void launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, void** args) {
+// Optional per-launch timing with HIP events recorded on the launch stream.
+struct ProfileRecord {
+  std::string name;
+  hipEvent_t start, stop;
+};
+std::mutex g_profile_lock;
+bool g_profile_on = false;
+std::vector<ProfileRecord> g_profile;
+
+void launch(const std::string& name, hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream,
+            void** args) {
+  ProfileRecord record{name, nullptr, nullptr};
+  bool timed;
+  {
+    std::lock_guard<std::mutex> guard(g_profile_lock);
+    timed = g_profile_on;
+  }
+  if (timed) {
+    check_hip(hipEventCreate(&record.start), "hipEventCreate");
+    check_hip(hipEventCreate(&record.stop), "hipEventCreate");
+    check_hip(hipEventRecord(record.start, stream), "hipEventRecord");
+  }
   check_hip(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, args,
                                   nullptr),
             "hipModuleLaunchKernel");
   check_hip(hipGetLastError(), "kernel launch");
+  if (timed) {
+    check_hip(hipEventRecord(record.stop, stream), "hipEventRecord");
+    std::lock_guard<std::mutex> guard(g_profile_lock);
+    g_profile.push_back(record);
+  }
 }
 
 template <typename F>
@@ -196,10 +223,10 @@ int luna_uvu_plan_destroy(LunaUvuPlan* plan) {
     if (!plan) return;
     for (auto& kv : plan->plan.modules) {
       int current = 0;
-      hipGetDevice(&current);
-      hipSetDevice(kv.first.second);
-      hipModuleUnload((hipModule_t)kv.second);
-      hipSetDevice(current);
+      (void)hipGetDevice(&current);
+      (void)hipSetDevice(kv.first.second);
+      (void)hipModuleUnload((hipModule_t)kv.second);
+      (void)hipSetDevice(current);
     }
     delete plan;
   });
@@ -226,7 +253,7 @@ int luna_uvu_plan_info(const LunaUvuPlan* plan, LunaUvuPlanInfo* info) {
 int luna_uvu_plan_precompile(LunaUvuPlan* plan) {
   return guarded([&] {
     if (!plan) fail("luna_uvu_plan_precompile: null plan");
-    for (const char* v : {"fwd00", "bwd00"}) code_for(plan->plan, v);
+    for (const char* v : {"fwd00", "bwd00111"}) code_for(plan->plan, v);
   });
 }
 
@@ -248,28 +275,39 @@ int luna_uvu_conv_fwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
     for (int phase = 0; phase < plan.fwd_phases; ++phase) {
       hipFunction_t f = function_for(module, "luna_uvu_fwd_p" + std::to_string(phase));
       void* args[] = {&x, &y, &w, &env, &src, &dst_rowptr, &node_order, &out, &l0};
-      launch(f, dim3((unsigned)num_nodes, (unsigned)plan.phase_slots[phase]), dim3(64),
-             (hipStream_t)stream, args);
+      launch("uvu_fwd_p" + std::to_string(phase), f,
+             dim3((unsigned)num_nodes, (unsigned)plan.phase_slots[phase]), dim3(64), (hipStream_t)stream,
+             args);
     }
   });
 }
+
+namespace {
+
+// Workspace layout: gy/genv partials, then the per-edge gx messages.
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+size_t part_bytes(const Plan& p, int64_t num_edges) {
+  return align256((size_t)p.gy_parts * (size_t)num_edges * (size_t)(p.spec.in2 + 1) * (p.spec.dtype_bits / 8));
+}
+size_t msg_bytes(const Plan& p, int64_t num_edges) {
+  return align256((size_t)num_edges * (size_t)p.spec.in1 * (p.spec.dtype_bits / 8));
+}
+
+}  // namespace
 
 int luna_uvu_conv_bwd_workspace(const LunaUvuPlan* plan, int64_t num_nodes, int64_t num_edges,
                                 size_t* bytes) {
   return guarded([&] {
     if (!plan || !bytes) fail("luna_uvu_conv_bwd_workspace: null argument");
-    (void)num_nodes;
-    const Plan& p = plan->plan;
-    const size_t real = p.spec.dtype_bits / 8;
-    // Partial columns include one for the envelope gradient.
-    *bytes = (size_t)p.gy_parts * (size_t)num_edges * (size_t)(p.spec.in2 + 1) * real;
+    if (num_nodes < 0 || num_edges < 0) fail("negative problem size");
+    *bytes = part_bytes(plan->plan, num_edges) + msg_bytes(plan->plan, num_edges);
   });
 }
 
 int luna_uvu_conv_bwd(const LunaUvuPlan* cplan, const void* x, const void* y, const void* w,
-                      const void* env, const void* g, const void* gl0, const int32_t* dst,
-                      const int32_t* src_rowptr, const int32_t* edge_ids_by_src,
-                      const int32_t* source_node_order, void* gx, void* gy, void* gw, void* genv,
+                      const void* env, const void* g, const void* gl0, const int32_t* src,
+                      const int32_t* dst_rowptr, const int32_t* node_order, const int32_t* src_rowptr,
+                      const int32_t* edge_ids_by_src, void* gx, void* gy, void* gw, void* genv,
                       void* workspace, size_t workspace_bytes, int64_t num_nodes, int64_t num_edges,
                       LunaStream stream) {
   return guarded([&] {
@@ -278,31 +316,91 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
     if (num_nodes < 0 || num_edges < 0) fail("negative problem size");
     if (num_nodes > 0x7fffffffLL || num_edges > 0x7fffffffLL) fail("graph exceeds int32 indexing");
     if (num_nodes == 0) return;
-    if (!x || !g || !src_rowptr || !source_node_order) fail("luna_uvu_conv_bwd: null tensor");
-    if (num_edges > 0 && (!y || !w || !dst || !edge_ids_by_src)) fail("luna_uvu_conv_bwd: null edge tensor");
+    if (!x || !g || !dst_rowptr || !node_order || !src_rowptr) fail("luna_uvu_conv_bwd: null tensor");
+    if (num_edges > 0 && (!y || !w || !src || !edge_ids_by_src)) fail("luna_uvu_conv_bwd: null edge tensor");
     if (gl0 && plan.spec.l0_dim == 0) gl0 = nullptr;
     if (!env) genv = nullptr;
-    size_t need = 0;
-    luna_uvu_conv_bwd_workspace(cplan, num_nodes, num_edges, &need);
-    const bool want_parts = (gy || genv) && num_edges > 0;
-    if (want_parts && (workspace_bytes < need || !workspace)) fail("luna_uvu_conv_bwd: workspace too small");
-    std::string variant = std::string("bwd") + (env ? '1' : '0') + (gl0 ? '1' : '0');
-    hipModule_t module = module_for(plan, variant);
     int64_t E = num_edges;
-    void* part = workspace;
-    for (int phase = 0; phase < plan.bwd_phases; ++phase) {
-      hipFunction_t f = function_for(module, "luna_uvu_bwd_p" + std::to_string(phase));
-      void* args[] = {&x, &y, &w, &env, &g, &gl0, &dst, &src_rowptr, &edge_ids_by_src,
-                      &source_node_order, &gx, &gw, &part, &E};
-      launch(f, dim3((unsigned)num_nodes, (unsigned)plan.bwd_phase_slots[phase]), dim3(64),
-             (hipStream_t)stream, args);
+    const bool want_parts = (gy || genv) && E > 0;
+    const bool want_msg = gx && E > 0;
+    const size_t pbytes = part_bytes(plan, E), mbytes = msg_bytes(plan, E);
+    if ((want_parts || want_msg) && (!workspace || workspace_bytes < pbytes + mbytes))
+      fail("luna_uvu_conv_bwd: workspace too small");
+    void* part = want_parts ? workspace : nullptr;
+    void* msg = want_msg ? (void*)((char*)workspace + pbytes) : nullptr;
+    std::string variant = std::string("bwd") + (env ? '1' : '0') + (gl0 ? '1' : '0') + (gw ? '1' : '0') +
+                          (want_msg ? '1' : '0') + (want_parts ? '1' : '0');
+    hipModule_t module = module_for(plan, variant);
+    hipStream_t s = (hipStream_t)stream;
+    if (want_msg && plan.bwd_gx_needs_zero) {
+      int64_t n = E * (int64_t)plan.spec.in1;
+      void* args[] = {&msg, &n};
+      launch("uvu_fill", function_for(module, "luna_uvu_fill"), dim3((unsigned)((n + 255) / 256)),
+             dim3(256), s, args);
+    }
+    if (E > 0 && (gw || want_parts || want_msg)) {
+      for (int phase = 0; phase < plan.bwd_phases; ++phase) {
+        hipFunction_t f = function_for(module, "luna_uvu_bwd_p" + std::to_string(phase));
+        void* args[] = {&x, &y, &w, &env, &g, &gl0, &src, &dst_rowptr, &node_order, &gw, &msg, &part, &E};
+        launch("uvu_bwd_p" + std::to_string(phase), f,
+               dim3((unsigned)num_nodes, (unsigned)plan.bwd_phase_slots[phase]), dim3(64), s, args);
+      }
     }
     if (want_parts) {
-      hipFunction_t f = function_for(module, "luna_uvu_bwd_reduce");
       const int64_t pw = plan.spec.in2 + (env ? 1 : 0);
       const int64_t total = E * pw;
       void* args[] = {&part, &gy, &genv, &E};
-      launch(f, dim3((unsigned)((total + 255) / 256)), dim3(256), (hipStream_t)stream, args);
+      launch("uvu_bwd_reduce", function_for(module, "luna_uvu_bwd_reduce"),
+             dim3((unsigned)((total + 255) / 256)), dim3(256), s, args);
+    }
+    if (gx) {
+      // With no edges the gather still writes zeros (every source row is empty).
+      void* args[] = {&msg, &src_rowptr, &edge_ids_by_src, &gx};
+      launch("uvu_bwd_gather", function_for(module, "luna_uvu_bwd_gather"),
+             dim3((unsigned)num_nodes, (unsigned)((plan.spec.in1 + 255) / 256)), dim3(256), s, args);
+    }
+  });
+}
+
+int luna_profile_enable(int on) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> guard(g_profile_lock);
+    g_profile_on = on != 0;
+  });
+}
+
+int luna_profile_collect(char* buffer, size_t capacity, size_t* needed) {
+  return guarded([&] {
+    std::vector<ProfileRecord> records;
+    {
+      std::lock_guard<std::mutex> guard(g_profile_lock);
+      records.swap(g_profile);
+    }
+    std::map<std::string, std::vector<float>> times;
+    for (auto& r : records) {
+      check_hip(hipEventSynchronize(r.stop), "hipEventSynchronize");
+      float ms = 0.f;
+      check_hip(hipEventElapsedTime(&ms, r.start, r.stop), "hipEventElapsedTime");
+      times[r.name].push_back(ms);
+      (void)hipEventDestroy(r.start);
+      (void)hipEventDestroy(r.stop);
+    }
+    std::ostringstream text;
+    for (auto& kv : times) {
+      double total = 0, lo = 1e30, hi = 0;
+      for (float t : kv.second) {
+        total += t;
+        lo = std::min(lo, (double)t);
+        hi = std::max(hi, (double)t);
+      }
+      text << kv.first << ' ' << kv.second.size() << ' ' << total << ' ' << lo << ' ' << hi << '\n';
+    }
+    std::string out = text.str();
+    if (needed) *needed = out.size() + 1;
+    if (buffer && capacity) {
+      size_t n = std::min(capacity - 1, out.size());
+      std::memcpy(buffer, out.data(), n);
+      buffer[n] = '\0';
     }
   });
 }

@@ -260,8 +260,7 @@ def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, T
     need_env = need_env and env is not None
     gx = gy = gw = genv = None
     if need_x:
-        factory = torch.zeros if plan.info.bwd_gx_needs_zero else torch.empty
-        gx = factory((N, op.in1_dim), device=x.device, dtype=x.dtype)
+        gx = torch.empty((N, op.in1_dim), device=x.device, dtype=x.dtype)
     if need_y:
         gy = torch.empty((E, op.in2_dim), device=x.device, dtype=x.dtype)
     if need_w:
@@ -274,13 +273,13 @@ def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, T
         _native.check(lib.luna_uvu_conv_bwd_workspace(plan.handle, N, E, ctypes.byref(size)),
                       "luna_uvu_conv_bwd_workspace")
         workspace = None
-        if (need_y or need_env) and E:
+        if (need_x or need_y or need_env) and E:
             workspace = torch.empty(size.value, device=x.device, dtype=torch.uint8)
         _native.check(lib.luna_uvu_conv_bwd(
             plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w), _native.ptr(env),
             g.data_ptr(), _native.ptr(gl0) if (gl0 is not None and gl0.numel()) else None,
-            graph.dst.data_ptr(), graph.src_rowptr.data_ptr(), graph.edge_ids_by_src.data_ptr(),
-            graph.source_node_order.data_ptr(),
+            graph.src.data_ptr(), graph.dst_rowptr.data_ptr(), graph.node_order.data_ptr(),
+            graph.src_rowptr.data_ptr(), graph.edge_ids_by_src.data_ptr(),
             _native.ptr(gx), _native.ptr(gy), _native.ptr(gw), _native.ptr(genv),
             _native.ptr(workspace), size.value if workspace is not None else 0,
             N, E, _stream(x)), "luna_uvu_conv_bwd")
