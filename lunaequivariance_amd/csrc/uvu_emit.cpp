@@ -19,6 +19,7 @@
 //   gy[e, yb + j] = sum_u w sum_i x_i q_ij      (partials per wave, then reduced)
 //   genv[e] = sum_u sum_k w g_k t_k, t_k = sum c x_i y_j
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -36,8 +37,10 @@ struct Code {
   std::ostringstream s;
   template <typename... A>
   __attribute__((format(printf, 2, 0))) void line(const char* fmt, A... args) {
-    char buffer[1024];
-    std::snprintf(buffer, sizeof(buffer), fmt, args...);
+    const int size = std::snprintf(nullptr, 0, fmt, args...);
+    std::string buffer(size + 1, '\0');
+    std::snprintf(&buffer[0], buffer.size(), fmt, args...);
+    buffer.resize(size);
     s << buffer << '\n';
   }
   void raw(const std::string& text) { s << text; }
@@ -160,6 +163,50 @@ std::string emit_butterfly(Code& c, std::vector<std::string> names, const char* 
   *shift = 6 - split_bits;
   *low_mask = (1 << (6 - split_bits)) - 1;
   return names[0];
+}
+
+// (i, j) pairs of one path grouped by their coefficient vector over k, equal
+// up to a global sign (relative tolerance 1e-12 absorbs last-bit differences
+// between equal Clebsch-Gordan values).
+struct ClassMember {
+  int i, j, sign;
+};
+struct SignedClass {
+  std::vector<std::pair<int, double>> coefficients;  // (k, c) of the representative
+  std::vector<ClassMember> members;
+};
+
+std::vector<SignedClass> signed_classes(const std::map<std::pair<int, int>, std::vector<const Term*>>& by_ij) {
+  std::vector<SignedClass> classes;
+  for (const auto& kv : by_ij) {
+    std::vector<std::pair<int, double>> vec;
+    for (const Term* t : kv.second) vec.push_back({t->k, t->c});
+    std::sort(vec.begin(), vec.end());
+    int found = -1, sign = 1;
+    for (size_t n = 0; n < classes.size() && found < 0; ++n) {
+      const auto& ref = classes[n].coefficients;
+      if (ref.size() != vec.size()) continue;
+      for (int s : {1, -1}) {
+        bool same = true;
+        for (size_t m = 0; m < vec.size() && same; ++m) {
+          const double a = ref[m].second, b = s * vec[m].second;
+          same = ref[m].first == vec[m].first && std::abs(a - b) <= 1e-12 * std::max(std::abs(a), std::abs(b));
+        }
+        if (same) {
+          found = (int)n;
+          sign = s;
+          break;
+        }
+      }
+    }
+    if (found < 0) {
+      classes.push_back({vec, {}});
+      found = (int)classes.size() - 1;
+      sign = 1;
+    }
+    classes[found].members.push_back({kv.first.first, kv.first.second, sign});
+  }
+  return classes;
 }
 
 void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, bool l0, const Options& opt) {
@@ -359,21 +406,28 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
     }
     for (int j : js) c.line("        real b%d = 0;", j);
     for (int i : is) c.line("        real a%d = 0;", i);
-    for (const auto& kv : by_ij) {
-      const int i = kv.first.first, j = kv.first.second;
+    // Pairs whose coefficient vectors over k agree up to sign share one q
+    // (the signed coefficient classes of src/lunatp/utils/layout.py:110-168).
+    std::vector<SignedClass> classes = signed_classes(by_ij);
+    for (size_t n = 0; n < classes.size(); ++n) {
+      const SignedClass& cls = classes[n];
       bool first = true;
-      for (const Term* t : kv.second) {
-        std::string coef = literal(t->c, bits);
-        std::string seed = scalar_seed ? std::string("S0") : "G" + std::to_string(b) + "_" + std::to_string(t->k);
+      for (const auto& kc : cls.coefficients) {
+        std::string coef = literal(kc.second, bits);
+        std::string seed = scalar_seed ? std::string("S0") : "G" + std::to_string(b) + "_" + std::to_string(kc.first);
         if (first) {
-          c.line("        real q%d_%d = %s * %s;", i, j, coef.c_str(), seed.c_str());
+          c.line("        real q%zu = %s * %s;", n, coef.c_str(), seed.c_str());
           first = false;
         } else {
-          c.line("        q%d_%d = FMA(%s, %s, q%d_%d);", i, j, coef.c_str(), seed.c_str(), i, j);
+          c.line("        q%zu = FMA(%s, %s, q%zu);", n, coef.c_str(), seed.c_str(), n);
         }
       }
-      c.line("        b%d = FMA(x%d, q%d_%d, b%d);", j, i, i, j, j);
-      c.line("        a%d = FMA(y%d, q%d_%d, a%d);", i, q.y_off + j, i, j, i);
+      for (const auto& member : cls.members) {
+        const int i = member.i, j = member.j;
+        const char* sign = member.sign > 0 ? "" : "-";
+        c.line("        b%d = FMA(%sx%d, q%zu, b%d);", j, sign, i, n, j);
+        c.line("        a%d = FMA(%sy%d, q%zu, a%d);", i, sign, q.y_off + j, n, i);
+      }
     }
     // gw = sum_i x_i a_i  (= sum_ij x_i y_j q_ij)
     bool first = true;
@@ -524,35 +578,24 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
       if (env) writers[spec.in2].push_back({g.gy_slot_base + chunk, col});
     }
   }
-  std::vector<int> begin(pw + 1, 0), slots, cols;
-  for (int col = 0; col < pw; ++col) {
-    begin[col] = (int)slots.size();
-    for (const auto& sc : writers[col]) {
-      slots.push_back(sc.first);
-      cols.push_back(sc.second);
-    }
-  }
-  begin[pw] = (int)slots.size();
-  auto table = [&](const char* name, const std::vector<int>& values) {
-    c.s << "__constant__ int " << name << "[" << std::max<size_t>(values.size(), 1) << "] = {";
-    for (int v : values) c.s << v << ",";
-    if (values.empty()) c.s << "0";
-    c.s << "};\n";
-  };
-  table("reduce_begin", begin);
-  table("reduce_slot", slots);
-  table("reduce_col", cols);
+  // One thread per edge; every output column is a fixed sum of partial columns.
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_bwd_reduce(");
   c.line("    const real* __restrict__ part, real* __restrict__ gy, real* __restrict__ genv, i64 E) {");
-  c.line("  const i64 idx = (i64)blockIdx.x * 256 + threadIdx.x;");
-  c.line("  if (idx >= E * %d) return;", pw);
-  c.line("  const i64 e = idx / %d;", pw);
-  c.line("  const int col = (int)(idx - e * %d);", pw);
-  c.line("  real acc = 0;");
-  c.line("  for (int n = reduce_begin[col]; n < reduce_begin[col + 1]; ++n)");
-  c.line("    acc += part[((i64)reduce_slot[n] * E + e) * PART_W + reduce_col[n]];");
-  c.line("  if (col < %d) { if (gy) gy[e * IN2 + col] = acc; }", spec.in2);
-  if (env) c.line("  else if (genv) genv[e] = acc;");
+  c.line("  const i64 e = (i64)blockIdx.x * 256 + threadIdx.x;");
+  c.line("  if (e >= E) return;");
+  for (int col = 0; col < pw; ++col) {
+    std::string sum;
+    for (const auto& sc : writers[col]) {
+      char term[128];
+      std::snprintf(term, sizeof(term), "part[((i64)%d * E + e) * PART_W + %d]", sc.first, sc.second);
+      sum += (sum.empty() ? "" : " + ") + std::string(term);
+    }
+    if (sum.empty()) sum = "(real)0";
+    if (col < spec.in2)
+      c.line("  if (gy) gy[e * IN2 + %d] = %s;", col, sum.c_str());
+    else
+      c.line("  if (genv) genv[e] = %s;", sum.c_str());
+  }
   c.line("}");
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_fill(real* __restrict__ p, i64 n) {");
   c.line("  const i64 i = (i64)blockIdx.x * 256 + threadIdx.x;");
@@ -578,18 +621,26 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     c.raw(";\n");
   }
   c.line("}");
+  const int vec = gather_vector_width(plan);
+  const char* vtype = vec == 1 ? "real" : (spec.dtype_bits == 64 ? "double2" : "float4");
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_bwd_gather(");
   c.line("    const real* __restrict__ msg, const int* __restrict__ srow, const int* __restrict__ ebs,");
   c.line("    real* __restrict__ gx) {");
+  c.line("  typedef %s vec_t;", vtype);
   c.line("  const int s = blockIdx.x;");
-  c.line("  const int col = blockIdx.y * 256 + threadIdx.x;");
+  c.line("  const int col = (blockIdx.y * 256 + threadIdx.x) * %d;", vec);
   c.line("  if (col >= IN1) return;");
-  c.line("  real acc = 0;");
+  c.line("  vec_t acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};");
   c.line("  if (covered(col)) {");
   c.line("    const int beg = srow[s], end = srow[s + 1];");
-  c.line("    for (int p = beg; p < end; ++p) acc += msg[(i64)ebs[p] * IN1 + col];");
+  c.line("    int p = beg;");
+  c.line("    for (; p + 4 <= end; p += 4) {");
+  for (int n = 0; n < 4; ++n)
+    c.line("      acc%d += *(const vec_t*)(msg + (i64)ebs[p + %d] * IN1 + col);", n, n);
+  c.line("    }");
+  c.line("    for (; p < end; ++p) acc0 += *(const vec_t*)(msg + (i64)ebs[p] * IN1 + col);");
   c.line("  }");
-  c.line("  gx[(i64)s * IN1 + col] = acc;");
+  c.line("  *(vec_t*)(gx + (i64)s * IN1 + col) = (acc0 + acc1) + (acc2 + acc3);");
   c.line("}");
   return c.s.str();
 }

@@ -71,6 +71,9 @@ struct Plan {
 };
 
 Spec parse_spec(const std::string& text);
+// Elements per access of the gx gather: 16-byte vectors when every covered
+// input range and the row length are multiples of it, else 1.
+int gather_vector_width(const Plan& plan);
 void build_schedule(Plan& plan);
 
 // Emitted HIP source of one kernel module variant.

@@ -347,17 +347,18 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
       }
     }
     if (want_parts) {
-      const int64_t pw = plan.spec.in2 + (env ? 1 : 0);
-      const int64_t total = E * pw;
       void* args[] = {&part, &gy, &genv, &E};
-      launch("uvu_bwd_reduce", function_for(module, "luna_uvu_bwd_reduce"),
-             dim3((unsigned)((total + 255) / 256)), dim3(256), s, args);
+      launch("uvu_bwd_reduce", function_for(module, "luna_uvu_bwd_reduce"), dim3((unsigned)((E + 255) / 256)),
+             dim3(256), s, args);
     }
     if (gx) {
       // With no edges the gather still writes zeros (every source row is empty).
       void* args[] = {&msg, &src_rowptr, &edge_ids_by_src, &gx};
+      const int vec = gather_vector_width(plan);
+      const int64_t per_block = 256LL * vec;
       launch("uvu_bwd_gather", function_for(module, "luna_uvu_bwd_gather"),
-             dim3((unsigned)num_nodes, (unsigned)((plan.spec.in1 + 255) / 256)), dim3(256), s, args);
+             dim3((unsigned)num_nodes, (unsigned)((plan.spec.in1 + per_block - 1) / per_block)), dim3(256), s,
+             args);
     }
   });
 }

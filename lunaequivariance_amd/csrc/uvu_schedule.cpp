@@ -184,6 +184,17 @@ int assign_phases(std::vector<Group>& groups, RangesOf ranges_of) {
 
 }  // namespace
 
+int gather_vector_width(const Plan& plan) {
+  const Spec& spec = plan.spec;
+  int vec = 16 / (spec.dtype_bits / 8);
+  bool aligned = spec.in1 % vec == 0;
+  for (const Group& g : plan.bwd_groups) {
+    const long end = g.x_off + (long)g.channels * g.d1;
+    aligned = aligned && g.x_off % vec == 0 && end % vec == 0;
+  }
+  return aligned ? vec : 1;
+}
+
 void build_schedule(Plan& plan) {
   const Spec& spec = plan.spec;
 
