@@ -240,3 +240,83 @@ def test_non_default_stream():
         result = conv(xd, yd, wd, graph=graph)
     stream.synchronize()
     assert_close(result, ref, dtype, "non-default stream")
+
+
+def load_golden(name):
+    import json
+    from pathlib import Path
+
+    import numpy as np
+
+    data = np.load(Path(__file__).resolve().parent / "golden" / f"{name}.npz")
+    meta = json.loads(str(data["meta"]))
+    meta["instructions"] = [tuple(i) for i in meta["instructions"]]
+    return meta, {k: torch.tensor(data[k]) for k in data.files if k != "meta"}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("name", ["reference_problem", "config1_small", "multi_edge_env", "lmax3_paths"])
+def test_golden_fixtures(name, dtype):
+    """HIP forward, first and second order against the committed oracle fixtures."""
+    meta, t = load_golden(name)
+    conv = make_conv(meta["in1"], meta["in2"], meta["out"], meta["instructions"], dtype)
+    graph = conv.create_graph(t["src"].to(DEV), t["dst"].to(DEV), meta["nodes"])
+    leaves = [t[k].to(DEV, dtype).requires_grad_() for k in ("x", "y", "w")]
+    env = t["env"].to(DEV, dtype) if "env" in t else None
+    out = conv(*leaves, graph=graph, env=env)
+    assert_close(out, t["out"], dtype, "forward")
+    first = torch.autograd.grad(out, leaves, t["g"].to(DEV, dtype), create_graph=True)
+    for a, k in zip(first, ("gx", "gy", "gw")):
+        assert_close(a, t[k], dtype, k)
+    second = torch.autograd.grad(first, leaves, tuple(t[k].to(DEV, dtype) for k in ("rx", "ry", "rw")))
+    for a, k in zip(second, ("hx", "hy", "hw")):
+        assert_close(a, t[k], dtype, k)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_full_size_sampled_rows(dtype):
+    """Config 2 (fp32) / config 3 (fp64) at full size: outputs and gradients of
+    sampled nodes and edges against the oracle evaluated on just those rows,
+    plus exact linearity of the forward in the weights."""
+    from lunaequivariance_amd.workloads import mace_irreps, periodic_radius_graph, spherical_harmonics
+
+    in1, sh, out, instructions = mace_irreps(128, 3)
+    conv = make_conv(in1, sh, out, instructions, dtype)
+    N = 20000
+    src, dst, _, vec, _ = periodic_radius_graph(N, 0.1, 5.0, seed=0, device=DEV)
+    E = src.numel()
+    assert E > 1_000_000
+    graph = conv.create_graph(src, dst, N)
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    x = torch.randn(N, conv.irreps_in1.dim, device=DEV, dtype=dtype, generator=gen).requires_grad_()
+    y = spherical_harmonics(3, vec).to(dtype).requires_grad_()
+    w = (torch.randn(E, conv.weight_numel, device=DEV, dtype=dtype, generator=gen) / 34 ** 0.5).requires_grad_()
+    g = torch.randn(N, conv.irreps_out.dim, device=DEV, dtype=dtype, generator=gen)
+    result = conv(x, y, w, graph=graph)
+    gx, gy, gw = torch.autograd.grad(result, (x, y, w), g)
+    with torch.no_grad():
+        doubled = conv(x, y, 2 * w, graph=graph)
+        assert torch.equal(doubled, 2 * result), "forward is not exactly linear in w"
+    pick = torch.randperm(N, generator=torch.Generator().manual_seed(1))[:12]
+    src_c, dst_c = src.cpu(), dst.cpu()
+    x64, y64, w64, g64 = (t.detach().double().cpu() for t in (x, y, w, g))
+    # Destination rows: forward, gw and gy of their in-edges.
+    for node in pick.tolist():
+        edges = torch.nonzero(dst_c == node).flatten()
+        local_dst = torch.zeros(len(edges), dtype=torch.long)
+        leaves = [x64.clone().requires_grad_(), y64[edges].clone().requires_grad_(),
+                  w64[edges].clone().requires_grad_()]
+        ref = uvu_conv(in1, sh, out, instructions, leaves[0], leaves[1], leaves[2], src_c[edges], local_dst, 1)
+        assert_close(result[node:node + 1], ref, dtype, f"out[{node}]")
+        rgx, rgy, rgw = torch.autograd.grad(ref, leaves, g64[node:node + 1])
+        assert_close(gy[edges.to(DEV)], rgy, dtype, f"gy of edges into {node}")
+        assert_close(gw[edges.to(DEV)], rgw, dtype, f"gw of edges into {node}")
+    # Source rows: gx sums the messages of a node's out-edges.
+    for node in pick[:4].tolist():
+        edges = torch.nonzero(src_c == node).flatten()
+        targets, local_dst = torch.unique(dst_c[edges], return_inverse=True)
+        xs = x64.clone().requires_grad_()
+        ref = uvu_conv(in1, sh, out, instructions, xs, y64[edges], w64[edges], src_c[edges], local_dst,
+                       len(targets))
+        (rgx,) = torch.autograd.grad(ref, xs, g64[targets])
+        assert_close(gx[node:node + 1], rgx[node:node + 1], dtype, f"gx[{node}]")
