@@ -44,6 +44,8 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--calibrate-copy", action="store_true",
+                        help="only run a 2 GiB device-to-device copy (HBM counter calibration)")
     parser.add_argument("--cpu-shard", type=int, default=400,
                         help="CPU baseline runs 1/shard of the destination rows")
     return parser.parse_args()
@@ -64,6 +66,10 @@ def main():
               "(the operator shards by destination-node ranges; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import lunaequivariance_amd as lunaeq
     from lunaequivariance_amd import _native
@@ -165,6 +171,24 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def calibrate_copy():
+    """Copy 2 GiB device-to-device five times: the HBM counters of this kernel
+    (reads 2 GiB, writes 2 GiB per launch) calibrate FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    n = 2 * 1024 ** 3 // 4
+    a = torch.ones(n, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    seconds = (time.perf_counter() - start) / 5
+    print(json.dumps({"copy_bytes_per_launch": 2 * n * 4, "copy_gbs": round(2 * n * 4 / seconds / 1e9, 1)}))
 
 
 def cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, shard, dtype):
