@@ -137,7 +137,9 @@ def main():
     if dominant and "gbs" in per_kernel[dominant]:
         achieved = per_kernel[dominant]["gbs"]
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic(args.config, dtype, dominant),
+                    "algorithmic_bytes": algo[dominant]}
     step_bytes = algo["uvu_fwd_p0"] + algo["uvu_bwd_p0"] + algo["uvu_bwd_reduce"]
 
     cpu = None
@@ -171,6 +173,22 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def measured_traffic(config, dtype, kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter
+    summary (FETCH_SIZE x2 and WRITE_SIZE x1 per the copy calibration), or None."""
+    import torch
+
+    name = f"hbm_traffic_{config}_{'fp32' if dtype == torch.float32 else 'fp64'}.json"
+    path = ROOT / "profiles" / name
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    entry = data["kernels"].get(kernel)
+    if entry is None:
+        return None
+    return round((entry["fetch_kib"] * data["fetch_scale"] + entry["write_kib"] * data["write_scale"]) * 1024)
 
 
 def calibrate_copy():
