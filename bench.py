@@ -34,7 +34,9 @@ CONFIGS = {
     "cfg2": dict(channels=128, atoms=20000, dtype="float32", double_backward=False),
     "cfg3": dict(channels=128, atoms=20000, dtype="float64", double_backward=False),
     "cfg4": dict(channels=64, atoms=10000, dtype="float32", double_backward=True),
+    "cfg5": dict(channels=64, rows=200000, dtype="float32"),
 }
+FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
 def parse_args():
@@ -74,6 +76,10 @@ def main():
     import lunaequivariance_amd as lunaeq
     from lunaequivariance_amd import _native
     from lunaequivariance_amd.workloads import mace_irreps, periodic_radius_graph, spherical_harmonics
+
+    if args.config == "cfg5":
+        bench_uvw(args)
+        return
 
     cfg = CONFIGS[args.config]
     dtype = getattr(torch, cfg["dtype"])
@@ -173,6 +179,71 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def bench_uvw(args):
+    """Config 5: shared-weight UVW 64x0e+64x1o+64x2e (x) SH l<=2 -> same, 200,000 rows,
+    forward + backward to x, y and the shared weight."""
+    import torch
+
+    import lunaequivariance_amd as lunaeq
+    from lunaequivariance_amd import _native
+    from lunaequivariance_amd.workloads import spherical_harmonics
+
+    cfg = CONFIGS["cfg5"]
+    ir, sh = "64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e"
+    a, b = lunaeq.Irreps(ir), lunaeq.Irreps(sh)
+    instructions = [(i, j, k, "uvw", True) for i, (_, x) in enumerate(a) for j, (_, y) in enumerate(b)
+                    for k, (_, z) in enumerate(a) if z in x * y]
+    tp = lunaeq.TensorProduct(ir, sh, ir, instructions, shared_weights=True, internal_weights=False)
+    device = torch.device("cuda:0")
+    torch.manual_seed(0)
+    rows = cfg["rows"]
+    x = torch.randn(rows, a.dim, device=device, requires_grad=True)
+    y = spherical_harmonics(2, torch.randn(rows, 3, device=device, dtype=torch.float64)).float().requires_grad_()
+    w = (torch.randn(tp.weight_numel, device=device) / 8.0).requires_grad_()
+    g = torch.randn(rows, a.dim, device=device)
+
+    def step():
+        out = tp(x, y, w)
+        return (out, *torch.autograd.grad(out, (x, y, w), g))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _native.profile_enable(True)
+    _native.profile_collect()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        result = step()
+        del result
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    _native.profile_enable(False)
+    kernels = _native.profile_collect()
+    ms = elapsed * 1000 / args.steps
+    sum_d3 = sum(2 * a[k].ir.l + 1 for _, _, k, _, _ in instructions)
+    gemm_flops = 2.0 * rows * sum_d3 * 64 * 64
+    flops = {"uvw_fwd": gemm_flops, "uvw_bwd_xy": gemm_flops, "uvw_bwd_w": gemm_flops / len(instructions)}
+    per_kernel = {}
+    for name, (count, total, low, high) in kernels.items():
+        entry = {"launches": count, "avg_ms": round(total / count, 4)}
+        if name in flops:
+            entry["tflops"] = round(flops[name] / (total / count / 1000) / 1e12, 2)
+        per_kernel[name] = entry
+    dominant = max(("uvw_fwd", "uvw_bwd_xy"), key=lambda n: kernels[n][1])
+    achieved = per_kernel[dominant]["tflops"]
+    print(json.dumps({
+        "metric": "UVW shared-weight TP rows/s fwd+bwd", "value": round(rows / (ms / 1000), 1), "unit": "rows/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random features, SH l<=2 of random unit vectors, random shared weights)",
+        "config": {"workload": "cfg5: UVW 64x0e+64x1o+64x2e x 1x0e+1x1o+1x2e -> same, shared weights, fwd+bwd",
+                   "rows": rows, "weight_numel": tp.weight_numel, "parallelism": "single GPU"},
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "kernels": per_kernel, "cpu_baseline": None,
+    }))
 
 
 def measured_traffic(config, dtype, kernel):

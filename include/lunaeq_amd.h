@@ -129,6 +129,47 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* plan,
                       void* workspace, size_t workspace_bytes,
                       int64_t num_nodes, int64_t num_edges, LunaStream stream);
 
+/* ------------------------------------------------------------------------ */
+/* Shared-weight UVW tensor product (fp32, matrix cores).                    */
+
+typedef struct LunaUvwPlan LunaUvwPlan;
+
+/*
+ * Build a UVW plan from its path specification (the metadata of
+ * build_uvw_metadata, src/lunatp/uvw/kernels/utils.py:100-190):
+ *   "LUNAUVW1 32 <in1> <in2> <out> <weight_numel> <npaths>"
+ *   then per path:
+ *   "<x_off> <y_off> <out_off> <w_off> <mul1> <mul2> <mul3> <d1> <d2> <d3> <nterms> (<i> <j> <k> <c>)*"
+ * Weights of a path are laid out [u][v][w] (e3nn).  Coefficients include the
+ * path weight.
+ * replaces: LunaTPUVW / load of the UVW extension (src/lunatp/interface.py:310-335)
+ */
+int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** plan);
+int luna_uvw_plan_destroy(LunaUvwPlan* plan);
+/* flags[0..3]: out, gx, gy, gw must be zero-filled by the caller (uncovered ranges). */
+int luna_uvw_plan_needs_zero(const LunaUvwPlan* plan, int32_t* flags);
+int luna_uvw_plan_precompile(LunaUvwPlan* plan);
+
+/*
+ * out[b] = sum over paths of the uvw product of x[b] [in1], y[b] [in2] with the
+ * shared weight [weight_numel], for b < rows.
+ * replaces: the UVW forward launcher (src/lunatp/uvw/kernels/forward.py:1576-1612)
+ */
+int luna_uvw_fwd(const LunaUvwPlan* plan, const void* x, const void* y, const void* weight,
+                 void* out, int64_t rows, LunaStream stream);
+
+/* Bytes of workspace luna_uvw_bwd needs when gw is requested. */
+int luna_uvw_bwd_workspace(const LunaUvwPlan* plan, int64_t rows, size_t* bytes);
+
+/*
+ * Backward of luna_uvw_fwd for seed g [rows, out]: gx and gy (both or neither)
+ * and gw [weight_numel] (NULL to skip; then workspace may be NULL).
+ * replaces: the UVW backward launcher (src/lunatp/uvw/interface.py:42-49)
+ */
+int luna_uvw_bwd(const LunaUvwPlan* plan, const void* x, const void* y, const void* weight,
+                 const void* g, void* gx, void* gy, void* gw, void* workspace,
+                 size_t workspace_bytes, int64_t rows, LunaStream stream);
+
 /*
  * Measurement hook (no counterpart in the reference): while enabled, every
  * launch is bracketed by HIP events on its stream.  luna_profile_collect waits

@@ -9,12 +9,12 @@ from .irreps import Irrep, Irreps
 from .layout import TensorProductConfig, TensorProductPaths, Instruction
 from .graph import LunaTPGraph, make_graph
 from .interface import prepare_tensor_product, tensor_product, tensor_product_conv
-from .modules import TensorProductConv
+from .modules import TensorProduct, TensorProductConv
 from .uvu_conv import create_uvu_conv_operator
 from .cg import wigner_3j
 
 __all__ = [
     "Irrep", "Irreps", "TensorProductConfig", "TensorProductPaths", "Instruction",
     "LunaTPGraph", "make_graph", "prepare_tensor_product", "tensor_product",
-    "tensor_product_conv", "TensorProductConv", "create_uvu_conv_operator", "wigner_3j",
+    "tensor_product_conv", "TensorProduct", "TensorProductConv", "create_uvu_conv_operator", "wigner_3j",
 ]

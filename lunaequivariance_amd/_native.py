@@ -37,6 +37,13 @@ PROTOTYPES = {
     "luna_uvu_conv_bwd_workspace": (ctypes.c_int, [_VP, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_uvu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 5 + [_VP] * 5
                           + [ctypes.c_size_t, _I64, _I64, _VP]),
+    "luna_uvw_plan_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_VP)]),
+    "luna_uvw_plan_destroy": (ctypes.c_int, [_VP]),
+    "luna_uvw_plan_needs_zero": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_int32)]),
+    "luna_uvw_plan_precompile": (ctypes.c_int, [_VP]),
+    "luna_uvw_fwd": (ctypes.c_int, [_VP] * 5 + [_I64, _VP]),
+    "luna_uvw_bwd_workspace": (ctypes.c_int, [_VP, _I64, ctypes.POINTER(ctypes.c_size_t)]),
+    "luna_uvw_bwd": (ctypes.c_int, [_VP] * 9 + [ctypes.c_size_t, _I64, _VP]),
     "luna_profile_enable": (ctypes.c_int, [ctypes.c_int]),
     "luna_profile_collect": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t,
                                              ctypes.POINTER(ctypes.c_size_t)]),

@@ -13,7 +13,7 @@ import subprocess
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
-SOURCES = ["uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp"]
+SOURCES = ["common.cpp", "uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp", "uvw.cpp"]
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wno-format-security",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -75,9 +75,23 @@ def standard_operators():
     return ops
 
 
+def uvw_operators():
+    """The shared-weight UVW layer of config 5 (fp32)."""
+    from .irreps import Irreps
+    from .layout import TensorProductPaths
+    from .uvw import LunaTPUVW
+
+    ir, sh = "64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e"
+    a, b = Irreps(ir), Irreps(sh)
+    instructions = [(i, j, k, "uvw", True) for i, (_, x) in enumerate(a) for j, (_, y) in enumerate(b)
+                    for k, (_, z) in enumerate(a) if z in x * y]
+    paths = TensorProductPaths(ir, sh, ir, instructions, shared_weights=True, internal_weights=False)
+    return [LunaTPUVW(paths)]
+
+
 def precompile() -> int:
     count = 0
-    for op in standard_operators():
+    for op in standard_operators() + uvw_operators():
         op.plan.precompile()
         count += 1
     return count

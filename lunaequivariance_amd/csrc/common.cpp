@@ -1,0 +1,245 @@
+// Shared runtime of the C-ABI library (see common.h).
+#include "common.h"
+
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <stdexcept>
+
+#include "../../include/lunaeq_amd.h"
+
+namespace luna {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Failure : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+uint64_t fnv1a(const std::string& text, uint64_t h = 1469598103934665603ULL) {
+  for (unsigned char ch : text) {
+    h ^= ch;
+    h *= 1099511628211ULL;
+  }
+  return h;
+}
+
+// Options for every emitted module.  Packed FP32 instructions are disabled.
+const char* kOptions[] = {
+    "--offload-arch=gfx950", "-O3", "-ffp-contract=fast", "-Xclang", "-target-feature",
+    "-Xclang", "-packed-fp32-ops", "-std=c++17",
+};
+constexpr int kNumOptions = sizeof(kOptions) / sizeof(kOptions[0]);
+
+struct ProfileRecord {
+  std::string name;
+  hipEvent_t start, stop;
+};
+std::mutex g_profile_lock;
+bool g_profile_on = false;
+std::vector<ProfileRecord> g_profile;
+
+}  // namespace
+
+void fail(const std::string& message) { throw Failure(message); }
+
+void check_hip(hipError_t status, const char* what) {
+  if (status != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+std::vector<char> compile_hip(const std::string& source, const std::string& cache_dir, const std::string& tag) {
+  std::string key_text = source;
+  for (int n = 0; n < kNumOptions; ++n) key_text += kOptions[n];
+  key_text += "luna-1";
+  char key[32];
+  std::snprintf(key, sizeof(key), "%016llx", (unsigned long long)fnv1a(key_text));
+  if (const char* dump = std::getenv("LUNAEQ_AMD_DUMP")) {
+    std::ofstream out(std::string(dump) + "/" + tag + "_" + key + ".hip");
+    out << source;
+  }
+  std::string path;
+  if (!cache_dir.empty()) {
+    path = cache_dir + "/" + tag + "_" + key + ".co";
+    std::ifstream in(path, std::ios::binary);
+    if (in) {
+      std::vector<char> data((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+      if (!data.empty()) return data;
+    }
+  }
+  hiprtcProgram program;
+  if (hiprtcCreateProgram(&program, source.c_str(), (tag + ".hip").c_str(), 0, nullptr, nullptr) !=
+      HIPRTC_SUCCESS)
+    fail("hiprtcCreateProgram failed");
+  hiprtcResult status = hiprtcCompileProgram(program, kNumOptions, kOptions);
+  if (status != HIPRTC_SUCCESS) {
+    size_t size = 0;
+    hiprtcGetProgramLogSize(program, &size);
+    std::string log(size, '\0');
+    if (size) hiprtcGetProgramLog(program, &log[0]);
+    hiprtcDestroyProgram(&program);
+    fail("hipRTC compilation of " + tag + " failed: " + log.substr(0, 4000));
+  }
+  size_t size = 0;
+  hiprtcGetCodeSize(program, &size);
+  std::vector<char> data(size);
+  hiprtcGetCode(program, data.data());
+  hiprtcDestroyProgram(&program);
+  if (!path.empty()) {
+    mkdir(cache_dir.c_str(), 0755);
+    // Write to a private name, then rename: concurrent builders never see a partial file.
+    std::string tmp = path + ".tmp" + std::to_string(getpid());
+    {
+      std::ofstream out(tmp, std::ios::binary);
+      out.write(data.data(), (std::streamsize)data.size());
+    }
+    std::rename(tmp.c_str(), path.c_str());
+  }
+  return data;
+}
+
+ModuleCache::~ModuleCache() {
+  int current = 0;
+  (void)hipGetDevice(&current);
+  for (auto& kv : modules) {
+    (void)hipSetDevice(kv.first.second);
+    (void)hipModuleUnload(kv.second);
+  }
+  if (!modules.empty()) (void)hipSetDevice(current);
+}
+
+const std::vector<char>& ModuleCache::code_for(const std::string& variant,
+                                               const std::function<std::string()>& source) {
+  std::lock_guard<std::mutex> guard(lock);
+  auto it = code.find(variant);
+  if (it != code.end()) return it->second;
+  std::vector<char> data = compile_hip(source(), cache_dir, tag + "_" + variant);
+  return code.emplace(variant, std::move(data)).first->second;
+}
+
+hipModule_t ModuleCache::module_for(const std::string& variant, const std::function<std::string()>& source) {
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  const std::vector<char>& data = code_for(variant, source);
+  std::lock_guard<std::mutex> guard(lock);
+  auto key = std::make_pair(variant, device);
+  auto it = modules.find(key);
+  if (it != modules.end()) return it->second;
+  hipModule_t module;
+  check_hip(hipModuleLoadData(&module, data.data()), "hipModuleLoadData");
+  modules[key] = module;
+  return module;
+}
+
+hipFunction_t function_for(hipModule_t module, const std::string& name) {
+  hipFunction_t function;
+  check_hip(hipModuleGetFunction(&function, module, name.c_str()), ("hipModuleGetFunction " + name).c_str());
+  return function;
+}
+
+void launch(const std::string& name, hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, void** args,
+            unsigned shared_bytes) {
+  ProfileRecord record{name, nullptr, nullptr};
+  bool timed;
+  {
+    std::lock_guard<std::mutex> guard(g_profile_lock);
+    timed = g_profile_on;
+  }
+  if (timed) {
+    check_hip(hipEventCreate(&record.start), "hipEventCreate");
+    check_hip(hipEventCreate(&record.stop), "hipEventCreate");
+    check_hip(hipEventRecord(record.start, stream), "hipEventRecord");
+  }
+  check_hip(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shared_bytes, stream,
+                                  args, nullptr),
+            "hipModuleLaunchKernel");
+  check_hip(hipGetLastError(), "kernel launch");
+  if (timed) {
+    check_hip(hipEventRecord(record.stop, stream), "hipEventRecord");
+    std::lock_guard<std::mutex> guard(g_profile_lock);
+    g_profile.push_back(record);
+  }
+}
+
+int guard_call(const std::function<void()>& body) {
+  try {
+    body();
+    g_last_error.clear();
+    return 0;
+  } catch (const std::exception& error) {
+    g_last_error = error.what();
+    return 1;
+  } catch (...) {
+    g_last_error = "unknown error";
+    return 1;
+  }
+}
+
+}  // namespace luna
+
+using namespace luna;
+
+extern "C" {
+
+const char* luna_last_error(void) { return g_last_error.c_str(); }
+
+const char* luna_version(void) { return "lunaeq_amd 0.2 gfx950"; }
+
+int luna_device_count(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+  return count;
+}
+
+int luna_profile_enable(int on) {
+  return guard_call([&] {
+    std::lock_guard<std::mutex> guard(g_profile_lock);
+    g_profile_on = on != 0;
+  });
+}
+
+int luna_profile_collect(char* buffer, size_t capacity, size_t* needed) {
+  return guard_call([&] {
+    std::vector<ProfileRecord> records;
+    {
+      std::lock_guard<std::mutex> guard(g_profile_lock);
+      records.swap(g_profile);
+    }
+    std::map<std::string, std::vector<float>> times;
+    for (auto& r : records) {
+      check_hip(hipEventSynchronize(r.stop), "hipEventSynchronize");
+      float ms = 0.f;
+      check_hip(hipEventElapsedTime(&ms, r.start, r.stop), "hipEventElapsedTime");
+      times[r.name].push_back(ms);
+      (void)hipEventDestroy(r.start);
+      (void)hipEventDestroy(r.stop);
+    }
+    std::ostringstream text;
+    for (auto& kv : times) {
+      double total = 0, lo = 1e30, hi = 0;
+      for (float t : kv.second) {
+        total += t;
+        lo = std::min(lo, (double)t);
+        hi = std::max(hi, (double)t);
+      }
+      text << kv.first << ' ' << kv.second.size() << ' ' << total << ' ' << lo << ' ' << hi << '\n';
+    }
+    std::string out = text.str();
+    if (needed) *needed = out.size() + 1;
+    if (buffer && capacity) {
+      size_t n = std::min(capacity - 1, out.size());
+      std::memcpy(buffer, out.data(), n);
+      buffer[n] = '\0';
+    }
+  });
+}
+
+}  // extern "C"

@@ -10,6 +10,8 @@
 #include <tuple>
 #include <vector>
 
+#include "common.h"
+
 namespace luna {
 
 // One sparse Clebsch-Gordan entry, already scaled by the path weight.
@@ -62,12 +64,7 @@ struct Plan {
   std::vector<int> bwd_phase_slots;  // grid.y per backward launch
   int gy_parts = 0;                  // partial slots for the gy reduction
   bool bwd_gx_needs_zero = false;
-  std::string cache_dir;
-
-  // Compiled code objects per variant key, and loaded modules per device.
-  std::mutex lock;
-  std::map<std::string, std::vector<char>> code;
-  std::map<std::pair<std::string, int>, void*> modules;  // (variant, device) -> hipModule_t
+  ModuleCache kernels;  // emitted modules per variant and device
 };
 
 Spec parse_spec(const std::string& text);
@@ -80,10 +77,5 @@ void build_schedule(Plan& plan);
 std::string emit_forward(const Plan& plan, bool env, bool l0);
 std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bool want_msg, bool want_part);
 
-// Compile HIP source for gfx950 with hipRTC, through the on-disk cache.
-std::vector<char> compile_hip(const std::string& source, const std::string& cache_dir,
-                              const std::string& tag);
-
-[[noreturn]] void fail(const std::string& message);
 
 }  // namespace luna

@@ -12,6 +12,62 @@ from .layout import TensorProductConfig
 from .uvu_conv import create_uvu_conv_operator
 
 
+class TensorProduct(torch.nn.Module):
+    """Row-wise tensor product (``src/modules/tensorproduct.py:19-116``).
+
+    This build provides the shared-weight ``uvw`` connection on matrix cores
+    (fp32); weights are the configuration's registered parameter unless given.
+    """
+
+    def __init__(self, irreps_in1, irreps_in2=None, irreps_out=None, instructions=None,
+                 in1_var=None, in2_var=None, out_var=None, irrep_normalization=None,
+                 path_normalization=None, internal_weights=None, shared_weights=None, *, dtype=None):
+        super().__init__()
+        if isinstance(irreps_in1, torch.nn.Module):
+            if any(value is not None for value in (
+                    irreps_in2, irreps_out, instructions, in1_var, in2_var, out_var,
+                    irrep_normalization, path_normalization, internal_weights, shared_weights)):
+                raise TypeError("Pass either an existing tensor product or irreps and path options")
+            tp = irreps_in1
+        else:
+            if irreps_in2 is None or irreps_out is None or instructions is None:
+                raise TypeError("irreps_in2, irreps_out and instructions are required")
+            tp = TensorProductConfig(
+                irreps_in1, irreps_in2, irreps_out, instructions,
+                in1_var=in1_var, in2_var=in2_var, out_var=out_var,
+                irrep_normalization=irrep_normalization, path_normalization=path_normalization,
+                internal_weights=internal_weights, shared_weights=shared_weights,
+            )
+            if dtype is not None and tp.weight.dtype != dtype:
+                tp.to(dtype=dtype)
+        modes = {ins.connection_mode for ins in tp.instructions}
+        if len(modes) != 1 or not modes <= {"uuu", "uvu", "uvw"}:
+            raise ValueError("TensorProduct requires one connection mode: uuu, uvu or uvw")
+        self.mode = modes.pop()
+        if self.mode != "uvw":
+            raise NotImplementedError(f"{self.mode} tensor products are not part of this MI355X build")
+        from .uvw import LunaTPUVW
+
+        weight = getattr(tp, "weight", None)
+        if dtype is None:
+            dtype = weight.dtype if isinstance(weight, torch.Tensor) and weight.numel() else torch.float32
+        self.op = LunaTPUVW(tp, dtype=dtype)
+        self.tp = tp
+        self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
+        self.instructions = tp.instructions
+        self.weight_numel = tp.weight_numel
+        self.internal_weights, self.shared_weights = tp.internal_weights, tp.shared_weights
+
+    @property
+    def weight(self):
+        return self.tp.weight
+
+    def forward(self, x, y, weight=None):
+        if weight is None and self.internal_weights:
+            weight = self.tp.weight
+        return self.op.run(x, y, weight)
+
+
 class TensorProductConv(torch.nn.Module):
     """Fused tensor product on every edge, summed at destination nodes.
 
@@ -92,4 +148,4 @@ class TensorProductConv(torch.nn.Module):
         return tensor_product_conv(x, edge_attr, weight, graph=graph, config=self.op, **kwargs)
 
 
-__all__ = ["TensorProductConv"]
+__all__ = ["TensorProduct", "TensorProductConv"]

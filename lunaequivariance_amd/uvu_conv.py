@@ -147,9 +147,12 @@ class NativePlan:
 
     def __del__(self):
         handle = getattr(self, "handle", None)
-        if handle is not None and _native._lib is not None:
-            _native._lib.luna_uvu_plan_destroy(handle)
-            self.handle = None
+        try:
+            if handle is not None and _native._lib is not None:
+                _native._lib.luna_uvu_plan_destroy(handle)
+        except Exception:  # interpreter shutdown
+            pass
+        self.handle = None
 
 
 class LunaTPUVUConv:

@@ -1,0 +1,241 @@
+"""Shared-weight UVW tensor product (matrix-core kernels, fp32).
+
+``out[b, io][w, k] = sum_paths pw * sum_{u,v} W[u, v, w] sum_{ij} c_ijk x[b, i1][u, i] y[b, i2][v, j]``
+with one weight tensor shared by every row (e3nn ``connection_mode="uvw"``,
+``shared_weights=True``; reference ``src/lunatp/uvw/interface.py:123-189`` and
+``uvw/kernels/utils.py:100-190``).  The library emits, per configuration, a
+forward and two backward kernels whose contractions over ``(u, v)`` and over
+rows run on ``v_mfma_f32_32x32x2f32``.  Autograd composes higher orders from
+the forward and backward kernels, as for the convolution.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from math import prod
+
+import torch
+
+from . import _native
+from .cg import sparse_terms
+from .layout import TensorProductPaths
+
+
+def build_uvw_metadata(tp, dtype=torch.float32) -> dict:
+    in_slices, y_slices, out_slices = tp.irreps_in1.slices(), tp.irreps_in2.slices(), tp.irreps_out.slices()
+    specs, offset = [], 0
+    for ins in tp.instructions:
+        if ins.connection_mode != "uvw":
+            raise ValueError(f"Only connection_mode='uvw' is supported, got {ins.connection_mode!r}.")
+        if not ins.has_weight:
+            raise ValueError("uvw generated kernels require weighted instructions.")
+        m1, ir1 = tp.irreps_in1[ins.i_in1]
+        m2, ir2 = tp.irreps_in2[ins.i_in2]
+        m3, ir3 = tp.irreps_out[ins.i_out]
+        if tuple(ins.path_shape) != (m1, m2, m3):
+            raise ValueError(f"Unexpected uvw path_shape={ins.path_shape}, expected {(m1, m2, m3)}.")
+        specs.append({
+            "x_offset": in_slices[ins.i_in1].start, "y_offset": y_slices[ins.i_in2].start,
+            "out_offset": out_slices[ins.i_out].start, "weight_offset": offset,
+            "in_channels": m1, "edge_channels": m2, "out_channels": m3,
+            "d1": ir1.dim, "d2": ir2.dim, "d3": ir3.dim, "l1": ir1.l, "l2": ir2.l, "l3": ir3.l,
+            "terms": sparse_terms(ir1.l, ir2.l, ir3.l, float(ins.path_weight)),
+        })
+        offset += prod(ins.path_shape)
+    if offset != tp.weight_numel:
+        raise ValueError(f"lowered weight_numel={offset}, configuration reports {tp.weight_numel}.")
+    return {"in1_dim": tp.irreps_in1.dim, "in2_dim": tp.irreps_in2.dim, "out_dim": tp.irreps_out.dim,
+            "weight_numel": tp.weight_numel, "weight_mode": "shared" if tp.shared_weights else "external",
+            "generated_specs": specs}
+
+
+def uvw_spec_text(meta: dict) -> str:
+    specs = meta["generated_specs"]
+    lines = [f"LUNAUVW1 32 {meta['in1_dim']} {meta['in2_dim']} {meta['out_dim']} {meta['weight_numel']} {len(specs)}"]
+    for s in specs:
+        head = (f"{s['x_offset']} {s['y_offset']} {s['out_offset']} {s['weight_offset']} {s['in_channels']} "
+                f"{s['edge_channels']} {s['out_channels']} {s['d1']} {s['d2']} {s['d3']} {len(s['terms'])}")
+        body = " ".join(f"{i} {j} {k} {float(c)!r}" for i, j, k, c in s["terms"])
+        lines.append(head + (" " + body if body else ""))
+    return "\n".join(lines) + "\n"
+
+
+class NativeUvwPlan:
+    def __init__(self, text: str):
+        lib = _native.lib()
+        handle = ctypes.c_void_p()
+        _native.check(lib.luna_uvw_plan_create(text.encode(), _native.cache_dir().encode(), ctypes.byref(handle)),
+                      "luna_uvw_plan_create")
+        self.handle = handle
+        flags = (ctypes.c_int32 * 4)()
+        _native.check(lib.luna_uvw_plan_needs_zero(handle, flags), "luna_uvw_plan_needs_zero")
+        self.out_zero, self.gx_zero, self.gy_zero, self.gw_zero = (bool(f) for f in flags)
+
+    def precompile(self):
+        _native.check(_native.lib().luna_uvw_plan_precompile(self.handle), "luna_uvw_plan_precompile")
+
+    def __del__(self):
+        handle = getattr(self, "handle", None)
+        try:
+            if handle is not None and _native._lib is not None:
+                _native._lib.luna_uvw_plan_destroy(handle)
+        except Exception:  # interpreter shutdown
+            pass
+        self.handle = None
+
+
+class LunaTPUVW:
+    """Prepared shared-weight UVW tensor product (``src/lunatp/interface.py:310-335``)."""
+
+    index_mode = "uvw"
+
+    def __init__(self, tp, *, dtype=None, index_bits=32):
+        tp = TensorProductPaths.from_tensor_product(tp)
+        self.tp = tp
+        self.compute_dtype = getattr(tp, "dtype", torch.float32) if dtype is None else dtype
+        if self.compute_dtype != torch.float32:
+            raise NotImplementedError("the matrix-core UVW tensor product runs in float32")
+        self.meta = build_uvw_metadata(tp, self.compute_dtype)
+        self.weight_mode = self.meta["weight_mode"]
+        if self.weight_mode != "shared":
+            raise NotImplementedError("UVW with per-row weights is not part of this build")
+        self.out_dim = self.meta["out_dim"]
+        self.spec = uvw_spec_text(self.meta)
+        self._plan = None
+
+    @property
+    def plan(self) -> NativeUvwPlan:
+        if self._plan is None:
+            self._plan = NativeUvwPlan(self.spec)
+        return self._plan
+
+    def run(self, x, y, weight):
+        return lunatp_uvw_func(self, x, y, weight)
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check(op, *tensors):
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError("UVW kernels run on the GPU; got a CPU tensor")
+        if t.dtype != op.compute_dtype:
+            raise ValueError(f"UVW inputs must use the initialized dtype {op.compute_dtype}")
+
+
+def run_forward(op, x, y, w):
+    _check(op, x, y, w)
+    rows = x.shape[0]
+    out = (torch.zeros if op.plan.out_zero else torch.empty)((rows, op.out_dim), device=x.device, dtype=x.dtype)
+    if rows:
+        _native.check(_native.lib().luna_uvw_fwd(op.plan.handle, x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                                 out.data_ptr(), rows, _stream(x)), "luna_uvw_fwd")
+    return out
+
+
+def run_backward(op, x, y, w, g, needs=(True, True, True)):
+    _check(op, x, y, w, g)
+    rows = x.shape[0]
+    plan = op.plan
+    want_xy = needs[0] or needs[1]
+    gx = gy = gw = None
+    if want_xy:
+        gx = (torch.zeros if plan.gx_zero else torch.empty)(x.shape, device=x.device, dtype=x.dtype)
+        gy = (torch.zeros if plan.gy_zero else torch.empty)(y.shape, device=x.device, dtype=x.dtype)
+    workspace = None
+    size = ctypes.c_size_t(0)
+    if needs[2]:
+        gw = (torch.zeros if plan.gw_zero else torch.empty)(w.shape, device=x.device, dtype=x.dtype)
+        _native.check(_native.lib().luna_uvw_bwd_workspace(plan.handle, rows, ctypes.byref(size)),
+                      "luna_uvw_bwd_workspace")
+        workspace = torch.empty(max(size.value, 4), device=x.device, dtype=torch.uint8)
+    if want_xy and rows == 0:
+        want_xy = False
+    if want_xy or needs[2]:
+        _native.check(_native.lib().luna_uvw_bwd(
+            plan.handle, x.data_ptr(), y.data_ptr(), w.data_ptr(), g.data_ptr(),
+            _native.ptr(gx) if want_xy else None, _native.ptr(gy) if want_xy else None, _native.ptr(gw),
+            _native.ptr(workspace), size.value, rows, _stream(x)), "luna_uvw_bwd")
+    return (gx if needs[0] else None, gy if needs[1] else None, gw)
+
+
+def _add(a, b):
+    return b if a is None else (a if b is None else a + b)
+
+
+class UVWForward(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, op, x, y, w):
+        ctx.op = op
+        ctx.save_for_backward(x, y, w)
+        ctx.set_materialize_grads(False)
+        return run_forward(op, x, y, w)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, y, w = ctx.saved_tensors
+        if g is None:
+            return None, None, None, None
+        needs = ctx.needs_input_grad[1:4]
+        grads = uvw_backward(ctx.op, x, y, w, g.contiguous(), needs)
+        return (None, *grads)
+
+
+class UVWBackward(torch.autograd.Function):
+    """(x, y, w, g) -> (gx, gy, gw); its derivative reuses the forward and backward kernels."""
+
+    @staticmethod
+    def forward(ctx, op, needs, x, y, w, g):
+        ctx.op = op
+        ctx.save_for_backward(x, y, w, g)
+        ctx.set_materialize_grads(False)
+        return run_backward(op, x, y, w, g, needs)
+
+    @staticmethod
+    def backward(ctx, rx, ry, rw):
+        x, y, w, g = ctx.saved_tensors
+        op = ctx.op
+        need = ctx.needs_input_grad  # (op, needs, x, y, w, g)
+        args = [x, y, w]
+        dirs = [None if r is None else r.contiguous() for r in (rx, ry, rw)]
+        grads = [None, None, None]
+        hg = None
+        for slot, direction in enumerate(dirs):
+            if direction is None:
+                continue
+            substituted = list(args)
+            substituted[slot] = direction
+            if need[5]:
+                hg = _add(hg, UVWForward.apply(op, *substituted))
+            wanted = tuple(need[2 + o] and o != slot for o in range(3))
+            if any(wanted):
+                parts = uvw_backward(op, *substituted, g, wanted)
+                for o in range(3):
+                    if wanted[o] and parts[o] is not None:
+                        grads[o] = _add(grads[o], parts[o])
+        return (None, None, *grads, hg)
+
+
+def uvw_backward(op, x, y, w, g, needs):
+    needs = tuple(bool(n) for n in needs)
+    if torch.is_grad_enabled():
+        return UVWBackward.apply(op, needs, x, y, w, g)
+    return run_backward(op, x, y, w, g, needs)
+
+
+def lunatp_uvw_func(op, x, y, weight):
+    """Shared-weight UVW product of rows x [B, in1] and y [B, in2] with weight [weight_numel]."""
+    if weight is None:
+        raise TypeError("UVW requires a weight tensor")
+    if x.ndim != 2 or y.ndim != 2:
+        raise ValueError("UVW x and edge_attr must be matrices")
+    if x.shape[1] != op.meta["in1_dim"] or y.shape != (x.shape[0], op.meta["in2_dim"]):
+        raise ValueError("UVW input shapes do not match the configuration")
+    if weight.shape != (op.meta["weight_numel"],):
+        raise ValueError(f"UVW expected weight shape {(op.meta['weight_numel'],)}, got {tuple(weight.shape)}")
+    return UVWForward.apply(op, x.contiguous(), y.contiguous(), weight.contiguous())
+
+
+__all__ = ["build_uvw_metadata", "uvw_spec_text", "LunaTPUVW", "lunatp_uvw_func"]

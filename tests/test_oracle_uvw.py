@@ -1,0 +1,103 @@
+"""CPU oracle of the shared-weight UVW tensor product (no GPU)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.uvu_conv import parse_irreps
+from oracle.uvw import uvw_path_weights, uvw_tensor_product
+from oracle.wigner import wigner_3j
+from tests.test_oracle_conv import block_diag_d, rotation
+
+
+def uvw_instructions(in1, in2, out):
+    a, b, c = parse_irreps(in1), parse_irreps(in2), parse_irreps(out)
+    return [(i, j, k, "uvw", True) for i, (_, l1, p1) in enumerate(a) for j, (_, l2, p2) in enumerate(b)
+            for k, (_, l3, p3) in enumerate(c) if abs(l1 - l2) <= l3 <= l1 + l2 and p1 * p2 == p3]
+
+
+def brute(in1, in2, out, instructions, x, y, w):
+    a, b, c = parse_irreps(in1), parse_irreps(in2), parse_irreps(out)
+    off = lambda irreps: np.cumsum([0] + [m * (2 * l + 1) for m, l, _ in irreps])
+    xo, yo, oo = off(a), off(b), off(c)
+    weights = uvw_path_weights(a, b, c, instructions)
+    result = np.zeros((x.shape[0], oo[-1]))
+    w_off = 0
+    for (i1, i2, io, *_), pw in zip(instructions, weights):
+        (m1, l1, _), (m2, l2, _), (m3, l3, _) = a[i1], b[i2], c[io]
+        cg = wigner_3j(l1, l2, l3)
+        for bb in range(x.shape[0]):
+            for u in range(m1):
+                for v in range(m2):
+                    for ww in range(m3):
+                        wt = w[w_off + (u * m2 + v) * m3 + ww]
+                        for i in range(2 * l1 + 1):
+                            for j in range(2 * l2 + 1):
+                                for k in range(2 * l3 + 1):
+                                    if cg[i, j, k] == 0:
+                                        continue
+                                    result[bb, oo[io] + ww * (2 * l3 + 1) + k] += (
+                                        pw * cg[i, j, k] * wt * x[bb, xo[i1] + u * (2 * l1 + 1) + i]
+                                        * y[bb, yo[i2] + v * (2 * l2 + 1) + j])
+        w_off += m1 * m2 * m3
+    return result
+
+
+def test_uvw_oracle_matches_brute_force():
+    in1, in2, out = "2x0e+2x1o", "1x0e+2x1o", "3x0e+2x1o+1x1e"
+    instructions = uvw_instructions(in1, in2, out)
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 8, generator=gen, dtype=torch.float64)
+    y = torch.randn(3, 7, generator=gen, dtype=torch.float64)
+    wn = sum(parse_irreps(in1)[i][0] * parse_irreps(in2)[j][0] * parse_irreps(out)[k][0]
+             for i, j, k, *_ in instructions)
+    w = torch.randn(wn, generator=gen, dtype=torch.float64)
+    dense = uvw_tensor_product(in1, in2, out, instructions, x, y, w)
+    assert np.allclose(dense.numpy(), brute(in1, in2, out, instructions, x.numpy(), y.numpy(), w.numpy()),
+                       atol=1e-12)
+
+
+def test_uvw_path_weights_match_package():
+    from lunaequivariance_amd import TensorProductConfig
+
+    in1 = out = "4x0e+4x1o+4x2e"
+    in2 = "1x0e+1x1o+1x2e"
+    instructions = uvw_instructions(in1, in2, out)
+    tp = TensorProductConfig(in1, in2, out, instructions, shared_weights=True)
+    expected = uvw_path_weights(parse_irreps(in1), parse_irreps(in2), parse_irreps(out), instructions)
+    assert [i.path_weight for i in tp.instructions] == pytest.approx(expected, rel=1e-14)
+    assert tp.weight.shape == (11 * 16,)
+
+
+def test_uvw_oracle_equivariance():
+    in1 = out = "3x0e+3x1o+3x2e"
+    in2 = "1x0e+1x1o+1x2e"
+    instructions = uvw_instructions(in1, in2, out)
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(4, 27, generator=gen, dtype=torch.float64)
+    y = torch.randn(4, 9, generator=gen, dtype=torch.float64)
+    w = torch.randn(len(instructions) * 9, generator=gen, dtype=torch.float64)
+    R = rotation(5)
+    rng = np.random.default_rng(6)
+    D1, D2 = block_diag_d(in1, R, rng), block_diag_d(in2, R, rng)
+    out_plain = uvw_tensor_product(in1, in2, out, instructions, x, y, w)
+    out_rot = uvw_tensor_product(in1, in2, out, instructions, x @ D1.T, y @ D2.T, w)
+    assert torch.allclose(out_rot, out_plain @ D1.T, atol=1e-10)
+
+
+def test_uvw_plan_compiles_without_gpu(tmp_path, monkeypatch):
+    """The matrix-core kernels of the config-5 layer are emitted and compiled for gfx950."""
+    import lunaequivariance_amd as lunaeq
+
+    monkeypatch.setenv("LUNAEQ_AMD_CACHE", str(tmp_path))
+    ir, sh = "64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e"
+    tp = lunaeq.TensorProduct(ir, sh, ir, uvw_instructions(ir, sh, ir), shared_weights=True,
+                              internal_weights=True)
+    assert tp.weight_numel == 45056
+    tp.op.plan.precompile()
+    assert len(list(tmp_path.glob("uvw_*.co"))) == 3
+    with pytest.raises(NotImplementedError):
+        lunaeq.TensorProduct(ir, sh, ir, uvw_instructions(ir, sh, ir), shared_weights=True,
+                             internal_weights=True, dtype=torch.float64)

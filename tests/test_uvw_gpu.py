@@ -1,0 +1,62 @@
+"""GPU parity of the matrix-core UVW tensor product against the fp64 oracle.
+
+Tolerance: max abs error <= 1e-5 * max|ref| + 1e-7 (fp32), for the forward
+and each derivative order.
+"""
+
+import pytest
+import torch
+
+import lunaequivariance_amd as lunaeq
+from oracle.uvw import uvw_tensor_product
+from tests.test_oracle_uvw import uvw_instructions
+from tests.test_uvu_conv_gpu import assert_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("in1,in2,out,rows", [
+    ("64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e", "64x0e+64x1o+64x2e", 100),     # config 5 layer
+    ("8x0e+8x1o", "1x0e+1x1o", "8x0e+8x1o+8x1e", 33),                       # narrow, padded tiles
+    ("96x0e+16x1o", "1x0e+2x1o", "48x0e+40x1o+8x2e", 70),                   # K > 64, mul2 = 2, odd mul3
+])
+def test_uvw_forward_and_two_orders(in1, in2, out, rows):
+    instructions = uvw_instructions(in1, in2, out)
+    tp = lunaeq.TensorProduct(in1, in2, out, instructions, shared_weights=True, internal_weights=False)
+    gen = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64) / 8
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ref = uvw_tensor_product(in1, in2, out, instructions, *ref_in)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in[:2], dev_in[2])
+    assert_close(act, ref, torch.float32, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    ref_first = torch.autograd.grad(ref, ref_in, g, create_graph=True)
+    dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32), create_graph=True)
+    for n, (a, r) in enumerate(zip(dev_first, ref_first)):
+        assert_close(a, r, torch.float32, f"first-order {n}")
+    dirs = [torch.randn(r.shape, generator=gen, dtype=torch.float64) for r in ref_first]
+    ref_second = torch.autograd.grad(ref_first, ref_in, dirs)
+    dev_second = torch.autograd.grad(dev_first, dev_in, [d.to(DEV, torch.float32) for d in dirs])
+    for n, (a, r) in enumerate(zip(dev_second, ref_second)):
+        assert_close(a, r, torch.float32, f"second-order {n}")
+
+
+def test_uvw_internal_weights_and_functional_api():
+    ir, sh = "16x0e+16x1o", "1x0e+1x1o"
+    instructions = uvw_instructions(ir, sh, ir)
+    tp = lunaeq.TensorProduct(ir, sh, ir, instructions, shared_weights=True, internal_weights=True).to(DEV)
+    x = torch.randn(40, tp.irreps_in1.dim, device=DEV)
+    y = torch.randn(40, tp.irreps_in2.dim, device=DEV)
+    out = tp(x, y)
+    ref = uvw_tensor_product(ir, sh, ir, instructions, x.double().cpu(), y.double().cpu(),
+                             tp.weight.detach().double().cpu())
+    assert_close(out, ref, torch.float32, "internal weights")
+    op = lunaeq.prepare_tensor_product(ir, sh, ir, instructions, shared_weights=True)
+    again = lunaeq.tensor_product(x, y, tp.weight.detach(), config=op)
+    assert_close(again, ref, torch.float32, "functional")
+    out.sum().backward()
+    assert tp.weight.grad is not None and tp.weight.grad.shape == (tp.weight_numel,)
