@@ -12,6 +12,7 @@ from .interface import prepare_tensor_product, tensor_product, tensor_product_co
 from .modules import TensorProduct, TensorProductConv
 from .uvu_conv import create_uvu_conv_operator
 from .cg import wigner_3j
+from . import ops  # registers the lunaeq_amd:: dispatcher operators
 
 __all__ = [
     "Irrep", "Irreps", "TensorProductConfig", "TensorProductPaths", "Instruction",

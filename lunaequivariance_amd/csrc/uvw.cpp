@@ -41,7 +41,7 @@ struct UvwSpec {
 };
 
 constexpr int kRows = 32;       // batch rows per workgroup tile
-constexpr int kChunkTiles = 32; // row tiles per workgroup in the weight-gradient pass
+constexpr int kChunkTiles = 8;  // row tiles per workgroup in the weight-gradient pass
 
 int read_int(std::istringstream& in, const char* what) {
   long long value;

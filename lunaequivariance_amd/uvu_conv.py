@@ -178,12 +178,17 @@ class LunaTPUVUConv:
         self.l0_offsets, self.l0_dim = l0_feature_layout(self.generated_specs)
         self.spec = spec_text(self.meta, dtype)
         self._plan = None
+        from .ops import operator_config
+
+        # JSON of the static configuration: the constant argument of the dispatcher ops.
+        self.torch_config = operator_config(self)
 
     @property
     def plan(self) -> NativePlan:
         if self._plan is None:
             self._plan = NativePlan(self.spec)
         return self._plan
+
 
     def run(self, x, edge_attr, weight, *, graph, env=None, return_l0_feat=False):
         return lunatp_uvu_conv_func(self, x, edge_attr, weight, graph=graph, env=env,
@@ -410,6 +415,13 @@ def lunatp_uvu_conv_func(op, x, edge_attr, weight, *, graph: LunaTPGraph, env=No
     weight = weight.contiguous()
     if env is not None:
         env = env.reshape(-1).contiguous()
+    if torch.compiler.is_compiling():
+        from . import ops
+
+        out, l0 = torch.ops.lunaeq_amd.uvu_conv_forward(
+            x, edge_attr, weight, env, ops.graph_tables(graph), graph.num_nodes, bool(return_l0_feat),
+            op.torch_config)
+        return (out, l0) if return_l0_feat else out
     return UVUConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
 
 
