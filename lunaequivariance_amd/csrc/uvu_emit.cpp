@@ -46,10 +46,21 @@ struct Code {
   void raw(const std::string& text) { s << text; }
 };
 
-// Emission switches, overridable through LUNAEQ_AMD_EMIT="prefetch=0,hoist=1,fwpe=2,bwpe=2".
+// Emission switches, overridable through LUNAEQ_AMD_EMIT="fpre=1,bpre=2,hoist=1,fwpe=2,bwpe=2".
 struct Options {
-  bool prefetch = true;  // software-pipeline the edge loops
+  int fwd_prefetch = 1;  // edge-loop software pipelining depth (0 none, 1 x/w, 2 all operands)
+  int bwd_prefetch = 2;
+  int prefetch = 0;      // the depth of the kernel being emitted
+  bool fwd_nt_w = true;  // stream the per-edge weights with non-temporal loads
+  bool bwd_nt_w = false;
+  bool nt_w = false;     // the setting of the kernel being emitted
+  bool nt_gw = true;     // non-temporal stores of the weight gradient
+  bool nt_msg = false;   // non-temporal stores of the gx messages
+  bool y_vgpr = true;    // copy y into vector registers before use: a scalar
+                         // operand makes a VALU op issue at half rate
   bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
+  int fwd_local = -1;    // forward in per-path form (no products shared between
+                         // paths): 1 on, 0 off, -1 for fp64 only
   int fwd_wpe = 0;       // amdgpu_waves_per_eu hint for the forward (0 = none)
   int bwd_wpe = 0;       // same for the backward
 };
@@ -64,7 +75,14 @@ Options options() {
     size_t at = s.find(k);
     return at == std::string::npos ? fallback : std::atoi(s.c_str() + at + k.size());
   };
-  o.prefetch = value("prefetch", o.prefetch) != 0;
+  o.fwd_prefetch = value("fpre", o.fwd_prefetch);
+  o.fwd_nt_w = value("fntw", o.fwd_nt_w) != 0;
+  o.bwd_nt_w = value("bntw", o.bwd_nt_w) != 0;
+  o.nt_gw = value("ntgw", o.nt_gw) != 0;
+  o.nt_msg = value("ntmsg", o.nt_msg) != 0;
+  o.y_vgpr = value("yv", o.y_vgpr) != 0;
+  o.fwd_local = value("flocal", o.fwd_local);
+  o.bwd_prefetch = value("bpre", o.bwd_prefetch);
   o.hoist = value("hoist", o.hoist) != 0;
   o.fwd_wpe = value("fwpe", o.fwd_wpe);
   o.bwd_wpe = value("bwpe", o.bwd_wpe);
@@ -74,6 +92,8 @@ Options options() {
 std::string literal(double c, int bits) {
   char buffer[64];
   if (bits == 64) {
+    // Wrapped so that each use materialises its constant where it is used (see
+    // KC in the prelude).
     std::snprintf(buffer, sizeof(buffer), "%.17e", c);
   } else {
     std::snprintf(buffer, sizeof(buffer), "%.9ef", (double)(float)c);
@@ -93,6 +113,13 @@ std::string prelude(const Spec& spec) {
   s << "#define WNUM " << spec.wnum << "LL\n";
   s << "#define L0DIM " << spec.l0_dim << "LL\n";
   s << "#define PART_W " << spec.in2 + 1 << "LL\n";
+  if (fp64) {
+    // A double literal cannot be an instruction operand: it lives in a scalar
+    // register pair.  Left alone, the compiler hoists all of a kernel's
+    // coefficients out of the edge loop and spills scalar registers into
+    // vector lanes; the opaque copy keeps each one local to its use.
+    s << "__device__ __forceinline__ double KC(double v) { asm volatile(\"\" : \"+s\"(v)); return v; }\n";
+  }
   // Lane exchange v[lane ^ M]: DPP quad permutes for M = 1, 2, a swizzle for
   // M = 4..16 (within 32 lanes) and a permute through LDS hardware for M = 32.
   s << R"(
@@ -209,16 +236,33 @@ std::vector<SignedClass> signed_classes(const std::map<std::pair<int, int>, std:
   return classes;
 }
 
-void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, bool l0, const Options& opt) {
-  const int bits = spec.dtype_bits;
-  GroupUse use = group_use(spec, g);
+
+// Edge loop shared by the forward and backward groups.  With prefetch level 2
+// the operands of edge e+1 (x block, path weights, y row, env) and the source
+// index of edge e+2 are requested while edge e computes; empty asm statements
+// that read them at the end of the iteration make the wait for them land
+// there, after the iteration's stores, instead of at the loop head, where the
+// wait would also cover the stores just issued.
+// Emits the copy of y[yi] into a vector register before its first use.
+struct YCopies {
+  bool on;
+  std::set<int> done;
+  void need(Code& c, int yi) {
+    if (on && done.insert(yi).second) c.line("      asm(\"\" : \"+v\"(y%d));", yi);
+  }
+};
+
+void emit_operand_waits(Code& c, const Group& g, const GroupUse& use, bool env) {
+  for (int i = 0; i < g.d1; ++i) c.line("      asm volatile(\"\" :: \"v\"(nx%d));", i);
+  for (size_t n = 0; n < g.paths.size(); ++n) c.line("      asm volatile(\"\" :: \"v\"(nw%zu));", n);
+  for (int yi : use.ys) c.line("      asm volatile(\"\" :: \"s\"(ny%d));", yi);
+  if (env) c.line("      asm volatile(\"\" :: \"s\"(nev));");
+  c.line("      asm volatile(\"\" :: \"s\"(sn));");
+}
+
+void emit_loop_open(Code& c, const Spec& spec, const Group& g, const GroupUse& use, bool env,
+                    const Options& opt, const std::vector<std::string>& resident = {}) {
   const int np = (int)g.paths.size();
-  c.line("    const int u = (slot - %d) * 64 + lane;", g.slot_base);
-  c.line("    const bool active = u < %d;", g.channels);
-  c.line("    const int uc = active ? u : %d;", g.channels - 1);
-  for (size_t b = 0; b < g.blocks.size(); ++b)
-    for (int k = 0; k < g.blocks[b].d3; ++k) c.line("    real A%zu_%d = 0;", b, k);
-  // Edge operands: the gathered x block (d1 values) and one weight per path.
   auto load_edge = [&](const char* edge, const char* srcv) {
     c.line("      {");
     c.line("        const real* xq = x + (i64)%s * IN1 + (%d + uc * %d);", srcv, g.x_off, g.d1);
@@ -226,22 +270,46 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
     c.line("        const real* wq = w + (i64)%s * WNUM;", edge);
     for (int n = 0; n < np; ++n) {
       const Path& q = spec.paths[g.paths[n]];
-      c.line("        nw%d = wq[%d + uc * %d];", n, q.w_off, q.w_stride);
+      if (opt.nt_w)
+        c.line("        nw%d = __builtin_nontemporal_load(wq + %d + uc * %d);", n, q.w_off, q.w_stride);
+      else
+        c.line("        nw%d = wq[%d + uc * %d];", n, q.w_off, q.w_stride);
+    }
+    if (opt.prefetch >= 2) {
+      c.line("        const real* yq = y + (i64)%s * IN2;", edge);
+      for (int yi : use.ys) c.line("        ny%d = yq[%d];", yi, yi);
+      if (env) c.line("        nev = env[%s];", edge);
     }
     c.line("      }");
   };
-  if (opt.prefetch) {
+  if (opt.prefetch >= 1) {
     c.line("    if (beg < end) {");
     for (int i = 0; i < g.d1; ++i) c.line("      real nx%d;", i);
     for (int n = 0; n < np; ++n) c.line("      real nw%d;", n);
+    if (opt.prefetch >= 2) {
+      for (int yi : use.ys) c.line("      real ny%d;", yi);
+      if (env) c.line("      real nev;");
+    }
     c.line("      int sn = src[beg];");
     load_edge("beg", "sn");
+    if (opt.prefetch >= 2) {
+      c.line("      sn = src[beg + 1 < end ? beg + 1 : beg];");
+      // Resolve the first edge's operands before the loop too, so that the
+      // loop head needs no wait on either incoming path.
+      emit_operand_waits(c, g, use, env);
+      for (const auto& name : resident) c.line("      asm volatile(\"\" :: \"v\"(%s));", name.c_str());
+    }
     c.line("      for (int e = beg; e < end; ++e) {");
     for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = nx%d;", i, i);
     for (int n = 0; n < np; ++n) c.line("      const real w%d = nw%d;", n, n);
+    if (opt.prefetch >= 2) {
+      for (int yi : use.ys) c.line("      real y%d = ny%d;", yi, yi);
+      if (env) c.line("      const real ev = nev;");
+    }
     c.line("      const int en = e + 1 < end ? e + 1 : e;");
-    c.line("      sn = src[en];");
+    if (opt.prefetch < 2) c.line("      sn = src[en];");
     load_edge("en", "sn");
+    if (opt.prefetch >= 2) c.line("      sn = src[en + 1 < end ? en + 1 : en];");
   } else {
     c.line("    {");
     c.line("      for (int e = beg; e < end; ++e) {");
@@ -254,9 +322,31 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
       c.line("      const real w%d = wr[%d + uc * %d];", n, q.w_off, q.w_stride);
     }
   }
-  c.line("      const real* yr = y + (i64)e * IN2;");
-  for (int yi : use.ys) c.line("      const real y%d = yr[%d];", yi, yi);
-  if (env) c.line("      const real ev = env[e];");
+  if (opt.prefetch < 2) {
+    c.line("      const real* yr = y + (i64)e * IN2;");
+    for (int yi : use.ys) c.line("      real y%d = yr[%d];", yi, yi);
+    if (env) c.line("      const real ev = env[e];");
+  }
+}
+
+void emit_loop_close(Code& c, const Spec& spec, const Group& g, const GroupUse& use, bool env,
+                     const Options& opt) {
+  (void)spec;
+  if (opt.prefetch >= 2) emit_operand_waits(c, g, use, env);
+  c.line("      }");
+  c.line("    }");
+}
+
+void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, bool l0, const Options& opt) {
+  const int bits = spec.dtype_bits;
+  GroupUse use = group_use(spec, g);
+  const int np = (int)g.paths.size();
+  c.line("    const int u = (slot - %d) * 64 + lane;", g.slot_base);
+  c.line("    const bool active = u < %d;", g.channels);
+  c.line("    const int uc = active ? u : %d;", g.channels - 1);
+  for (size_t b = 0; b < g.blocks.size(); ++b)
+    for (int k = 0; k < g.blocks[b].d3; ++k) c.line("    real A%zu_%d = 0;", b, k);
+  emit_loop_open(c, spec, g, use, env, opt);
   // l0 columns are summed over the paths (edge copies) sharing them.
   std::map<int, std::vector<int>> l0_cols;
   for (int n = 0; n < np; ++n) {
@@ -272,13 +362,37 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
     return spec.paths[g.paths[a]].y_off < spec.paths[g.paths[b]].y_off;
   });
   std::set<std::pair<int, int>> formed;
+  YCopies ycopy{opt.y_vgpr, {}};
   for (int n : order) {
     const Path& q = spec.paths[g.paths[n]];
     const int b = g.path_block[n];
+    if (opt.fwd_local && !(l0 && q.l0_col >= 0)) {
+      // Per-path form: u_i = w x_i, then A_k += c (u_i y_j).  Nothing is
+      // shared between paths, so no product outlives its path (fewer live
+      // registers for about a third more arithmetic).
+      c.line("      {");
+      std::set<int> is;
+      for (const Term& t : q.terms) is.insert(t.i);
+      for (int i : is) c.line("        const real u%d = %s * x%d;", i, env ? ("w" + std::to_string(n) + " * ev").c_str() : ("w" + std::to_string(n)).c_str(), i);
+      std::map<std::pair<int, int>, std::vector<const Term*>> by_ij;
+      for (const Term& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
+      for (const auto& kv : by_ij) {
+        ycopy.need(c, q.y_off + kv.first.second);
+        c.line("        {");
+        c.line("          const real p = u%d * y%d;", kv.first.first, q.y_off + kv.first.second);
+        for (const Term* t : kv.second)
+          c.line("          A%d_%d = FMA(%s, p, A%d_%d);", b, t->k, literal(t->c, bits).c_str(), b, t->k);
+        c.line("        }");
+      }
+      c.line("      }");
+      continue;
+    }
     for (const Term& t : q.terms) {
       auto key = std::make_pair(t.i, q.y_off + t.j);
-      if (formed.insert(key).second)
+      if (formed.insert(key).second) {
+        ycopy.need(c, key.second);
         c.line("      const real p%d_%d = x%d * y%d;", key.first, key.second, key.first, key.second);
+      }
     }
     c.line("      {");
     if (env)
@@ -306,8 +420,7 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
   }
   for (const auto& col : l0_cols)
     c.line("      l0[(i64)e * L0DIM + %d + uc] = L%d;", col.first, col.first);
-  c.line("      }");
-  c.line("    }");
+  emit_loop_close(c, spec, g, use, env, opt);
   c.line("    if (active) {");
   for (size_t b = 0; b < g.blocks.size(); ++b) {
     const AccBlock& blk = g.blocks[b];
@@ -343,52 +456,37 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
       seeds.push_back("G" + std::to_string(b) + "_" + std::to_string(k));
     }
   }
-  auto load_edge = [&](const char* edge, const char* srcv) {
-    c.line("      {");
-    c.line("        const real* xq = x + (i64)%s * IN1 + (%d + uc * %d);", srcv, g.x_off, g.d1);
-    for (int i = 0; i < g.d1; ++i) c.line("        nx%d = xq[%d];", i, i);
-    c.line("        const real* wq = w + (i64)%s * WNUM;", edge);
-    for (int n = 0; n < np; ++n) {
-      const Path& q = spec.paths[g.paths[n]];
-      c.line("        nw%d = wq[%d + uc * %d];", n, q.w_off, q.w_stride);
-    }
-    c.line("      }");
-  };
-  if (opt.prefetch) {
-    c.line("    if (beg < end) {");
-    for (int i = 0; i < g.d1; ++i) c.line("      real nx%d;", i);
-    for (int n = 0; n < np; ++n) c.line("      real nw%d;", n);
-    c.line("      int sn = src[beg];");
-    load_edge("beg", "sn");
-    c.line("      for (int e = beg; e < end; ++e) {");
-    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = nx%d;", i, i);
-    for (int n = 0; n < np; ++n) c.line("      const real w%d = nw%d;", n, n);
-    c.line("      const int en = e + 1 < end ? e + 1 : e;");
-    c.line("      sn = src[en];");
-    load_edge("en", "sn");
-  } else {
-    c.line("    {");
-    c.line("      for (int e = beg; e < end; ++e) {");
-    c.line("      const int s = src[e];");
-    c.line("      const real* xr = x + (i64)s * IN1 + (%d + uc * %d);", g.x_off, g.d1);
-    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = xr[%d];", i, i);
-    c.line("      const real* wr = w + (i64)e * WNUM;");
-    for (int n = 0; n < np; ++n) {
-      const Path& q = spec.paths[g.paths[n]];
-      c.line("      const real w%d = wr[%d + uc * %d];", n, q.w_off, q.w_stride);
-    }
-  }
+  emit_loop_open(c, spec, g, use, env, opt, seeds);
   if (!opt.hoist) {
     // Opaque to the optimiser: keeps the edge-invariant q_ij inside the loop
     // instead of holding all of them in registers across it.
     for (const auto& name : seeds) c.line("      asm volatile(\"\" : \"+v\"(%s));", name.c_str());
   }
-  c.line("      const real* yr = y + (i64)e * IN2;");
-  for (int yi : use.ys) c.line("      const real y%d = yr[%d];", yi, yi);
-  if (env) c.line("      const real ev = env[e];");
+  YCopies ycopy{opt.y_vgpr, {}};
   for (int i = 0; i < g.d1; ++i) c.line("      real M%d = 0;", i);
   for (int yi : use.ys) c.line("      real GY%d = 0;", yi);
   if (env) c.line("      real GE = 0;");
+  // Partial-slot column of each gy (and genv) value: the y indices in order,
+  // then env.
+  std::map<std::string, int> column;
+  for (int yi : use.ys) column["GY" + std::to_string(yi)] = (int)column.size();
+  if (env) column["GE"] = (int)column.size();
+  // gy (and genv) partials of this wave: reduce `values` over the 64 channels
+  // and store them to their columns (consecutive from the first one).
+  int flush_id = 0;
+  auto flush = [&](const std::vector<std::string>& values) {
+    if (!want_part || values.empty()) return;
+    const std::string tag = "r" + std::to_string(flush_id++) + "_";
+    c.line("      {");
+    for (const auto& v : values) c.line("        %s = active ? %s : (real)0;", v.c_str(), v.c_str());
+    int shift = 0, low = 0;
+    std::string total = emit_butterfly(c, values, tag.c_str(), &shift, &low);
+    c.line("        const int col = lane >> %d;", shift);
+    c.line("        if ((lane & %d) == 0 && col < %zu)", low, values.size());
+    c.line("          part[((i64)(%d + (slot - %d)) * E + e) * PART_W + %d + col] = %s;", g.gy_slot_base,
+           g.slot_base, column[values[0]], total.c_str());
+    c.line("      }");
+  };
   for (int n = 0; n < np; ++n) {
     const Path& q = spec.paths[g.paths[n]];
     const int b = g.path_block[n];
@@ -426,6 +524,7 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
         const int i = member.i, j = member.j;
         const char* sign = member.sign > 0 ? "" : "-";
         c.line("        b%d = FMA(%sx%d, q%zu, b%d);", j, sign, i, n, j);
+        ycopy.need(c, q.y_off + j);
         c.line("        a%d = FMA(%sy%d, q%zu, a%d);", i, sign, q.y_off + j, n, i);
       }
     }
@@ -448,9 +547,11 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
         for (const Term& t : q.terms) {
           std::string coef = literal(t.c, bits);
           if (f2) {
+            ycopy.need(c, q.y_off + t.j);
             c.line("        real t0 = %s * (x%d * y%d);", coef.c_str(), t.i, q.y_off + t.j);
             f2 = false;
           } else {
+            ycopy.need(c, q.y_off + t.j);
             c.line("        t0 = FMA(%s, x%d * y%d, t0);", coef.c_str(), t.i, q.y_off + t.j);
           }
         }
@@ -466,7 +567,12 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
     } else {
       c.line("        const real ws = wv;");
     }
-    if (want_gw) c.line("        gw[(i64)e * WNUM + %d + uc * %d] = gwv;", q.w_off, q.w_stride);
+    if (want_gw) {
+      if (opt.nt_gw)
+        c.line("        __builtin_nontemporal_store(gwv, gw + (i64)e * WNUM + %d + uc * %d);", q.w_off, q.w_stride);
+      else
+        c.line("        gw[(i64)e * WNUM + %d + uc * %d] = gwv;", q.w_off, q.w_stride);
+    }
     for (int j : js) c.line("        GY%d = FMA(ws, b%d, GY%d);", q.y_off + j, j, q.y_off + j);
     for (int i : is) c.line("        M%d = FMA(ws, a%d, M%d);", i, i, i);
     c.line("      }");
@@ -479,28 +585,18 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
     for (int i = 0; i < g.d1; ++i) {
       if (g.gx_accumulate)
         c.line("        mr[%d] += M%d;", i, i);
+      else if (opt.nt_msg)
+        c.line("        __builtin_nontemporal_store(M%d, mr + %d);", i, i);
       else
         c.line("        mr[%d] = M%d;", i, i);
     }
     c.line("      }");
   }
-  // gy (and genv) partials of this wave: reduce over the 64 channels.
   std::vector<std::string> values;
   for (int yi : use.ys) values.push_back("GY" + std::to_string(yi));
   if (env) values.push_back("GE");
-  if (want_part && !values.empty()) {
-    c.line("      {");
-    for (const auto& v : values) c.line("        %s = active ? %s : (real)0;", v.c_str(), v.c_str());
-    int shift = 0, low = 0;
-    std::string total = emit_butterfly(c, values, "r", &shift, &low);
-    c.line("        const int col = lane >> %d;", shift);
-    c.line("        if ((lane & %d) == 0 && col < %zu)", low, values.size());
-    c.line("          part[((i64)(%d + (slot - %d)) * E + e) * PART_W + col] = %s;", g.gy_slot_base, g.slot_base,
-           total.c_str());
-    c.line("      }");
-  }
-  c.line("      }");
-  c.line("    }");
+  flush(values);
+  emit_loop_close(c, spec, g, use, env, opt);
 }
 
 std::string kernel_attributes(int wpe) {
@@ -512,20 +608,31 @@ std::string kernel_attributes(int wpe) {
 
 std::string emit_forward(const Plan& plan, bool env, bool l0) {
   const Spec& spec = plan.spec;
-  const Options opt = options();
+  Options opt = options();
+  opt.prefetch = opt.fwd_prefetch;
+  opt.nt_w = opt.fwd_nt_w;
+  if (opt.fwd_local < 0) opt.fwd_local = spec.dtype_bits == 64;
   Code c;
   c.raw(prelude(spec));
   for (int phase = 0; phase < plan.fwd_phases; ++phase) {
-    c.line("extern \"C\" __global__ void __launch_bounds__(64) %sluna_uvu_fwd_p%d(",
+    const int waves = plan.fwd_block_waves[phase], slots = plan.phase_slots[phase];
+    c.line("extern \"C\" __global__ void __launch_bounds__(%d) %sluna_uvu_fwd_p%d(", 64 * std::max(waves, 1),
            kernel_attributes(opt.fwd_wpe).c_str(), phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
     c.line("    const real* __restrict__ env, const int* __restrict__ src, const int* __restrict__ rowptr,");
     c.line("    const int* __restrict__ order, real* __restrict__ out, real* __restrict__ l0) {");
-    c.line("  const int lane = threadIdx.x;");
-    c.line("  const int t = order[blockIdx.x];");
+    if (waves == 0) {
+      // One wave per workgroup, the slots of a node on consecutive workgroups.
+      c.line("  const int lane = threadIdx.x;");
+      c.line("  const int t = order[blockIdx.x / %d];", slots);
+      c.line("  const int slot = blockIdx.x %% %d;", slots);
+    } else {
+      c.line("  const int lane = threadIdx.x & 63;");
+      c.line("  const int t = order[blockIdx.x];");
+      c.line("  const int slot = blockIdx.y * %d + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);", waves);
+    }
     c.line("  const int beg = rowptr[t];");
     c.line("  const int end = rowptr[t + 1];");
-    c.line("  const int slot = blockIdx.y;");
     bool first = true;
     for (const Group& g : plan.fwd_groups) {
       if (g.phase != phase) continue;
@@ -541,21 +648,31 @@ std::string emit_forward(const Plan& plan, bool env, bool l0) {
 
 std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bool want_msg, bool want_part) {
   const Spec& spec = plan.spec;
-  const Options opt = options();
+  Options opt = options();
+  opt.prefetch = opt.bwd_prefetch;
+  opt.nt_w = opt.bwd_nt_w;
   Code c;
   c.raw(prelude(spec));
   for (int phase = 0; phase < plan.bwd_phases; ++phase) {
-    c.line("extern \"C\" __global__ void __launch_bounds__(64) %sluna_uvu_bwd_p%d(",
+    const int waves = plan.bwd_block_waves[phase], slots = plan.bwd_phase_slots[phase];
+    c.line("extern \"C\" __global__ void __launch_bounds__(%d) %sluna_uvu_bwd_p%d(", 64 * std::max(waves, 1),
            kernel_attributes(opt.bwd_wpe).c_str(), phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
     c.line("    const real* __restrict__ env, const real* __restrict__ g, const real* __restrict__ gl0,");
     c.line("    const int* __restrict__ src, const int* __restrict__ rowptr, const int* __restrict__ order,");
     c.line("    real* __restrict__ gw, real* __restrict__ msg, real* __restrict__ part, i64 E) {");
-    c.line("  const int lane = threadIdx.x;");
-    c.line("  const int t = order[blockIdx.x];");
+    if (waves == 0) {
+      // One wave per workgroup, the slots of a node on consecutive workgroups.
+      c.line("  const int lane = threadIdx.x;");
+      c.line("  const int t = order[blockIdx.x / %d];", slots);
+      c.line("  const int slot = blockIdx.x %% %d;", slots);
+    } else {
+      c.line("  const int lane = threadIdx.x & 63;");
+      c.line("  const int t = order[blockIdx.x];");
+      c.line("  const int slot = blockIdx.y * %d + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);", waves);
+    }
     c.line("  const int beg = rowptr[t];");
     c.line("  const int end = rowptr[t + 1];");
-    c.line("  const int slot = blockIdx.y;");
     bool first = true;
     for (const Group& g : plan.bwd_groups) {
       if (g.phase != phase) continue;

@@ -64,6 +64,10 @@ struct Plan {
   std::vector<int> bwd_phase_slots;  // grid.y per backward launch
   int gy_parts = 0;                  // partial slots for the gy reduction
   bool bwd_gx_needs_zero = false;
+  // Waves per workgroup of each launch: the slots (waves) of one node share a
+  // workgroup, so they run on one CU and stream the node's contiguous weight
+  // rows together; grid = (nodes, ceil(slots / waves)).
+  std::vector<int> fwd_block_waves, bwd_block_waves;
   ModuleCache kernels;  // emitted modules per variant and device
 };
 

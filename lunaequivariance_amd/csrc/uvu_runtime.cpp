@@ -1,4 +1,5 @@
 // C-ABI entry points of the UVU convolution: plan lifetime and launchers.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 
@@ -31,6 +32,15 @@ size_t part_bytes(const Plan& p, int64_t num_edges) {
 }
 size_t msg_bytes(const Plan& p, int64_t num_edges) {
   return align256((size_t)num_edges * (size_t)p.spec.in1 * (p.spec.dtype_bits / 8));
+}
+
+// waves == 0: one wave per workgroup on a 1-D grid, slot fastest.
+dim3 grid_for(int64_t nodes, int slots, int waves) {
+  if (waves == 0) {
+    if (nodes * slots > 0x7fffffffLL) fail("launch grid exceeds 2^31 workgroups");
+    return dim3((unsigned)(nodes * slots));
+  }
+  return dim3((unsigned)nodes, (unsigned)((slots + waves - 1) / waves));
 }
 
 void check_sizes(int64_t num_nodes, int64_t num_edges) {
@@ -102,8 +112,8 @@ int luna_uvu_conv_fwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
       hipFunction_t f = function_for(module, "luna_uvu_fwd_p" + std::to_string(phase));
       void* args[] = {&x, &y, &w, &env, &src, &dst_rowptr, &node_order, &out, &l0};
       launch("uvu_fwd_p" + std::to_string(phase), f,
-             dim3((unsigned)num_nodes, (unsigned)plan.phase_slots[phase]), dim3(64), (hipStream_t)stream,
-             args);
+             grid_for(num_nodes, plan.phase_slots[phase], plan.fwd_block_waves[phase]),
+             dim3(64 * std::max(plan.fwd_block_waves[phase], 1)), (hipStream_t)stream, args);
     }
   });
 }
@@ -155,7 +165,8 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
         hipFunction_t f = function_for(module, "luna_uvu_bwd_p" + std::to_string(phase));
         void* args[] = {&x, &y, &w, &env, &g, &gl0, &src, &dst_rowptr, &node_order, &gw, &msg, &part, &E};
         launch("uvu_bwd_p" + std::to_string(phase), f,
-               dim3((unsigned)num_nodes, (unsigned)plan.bwd_phase_slots[phase]), dim3(64), s, args);
+               grid_for(num_nodes, plan.bwd_phase_slots[phase], plan.bwd_block_waves[phase]),
+               dim3(64 * std::max(plan.bwd_block_waves[phase], 1)), s, args);
       }
     }
     if (want_parts) {

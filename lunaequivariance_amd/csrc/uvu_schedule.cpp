@@ -22,7 +22,8 @@ namespace {
 
 constexpr int kWave = 64;
 // Upper bound on live output accumulators per lane for one group.
-constexpr int kMaxAccumulators = 64;
+// Accumulator budget per wave, in 32-bit registers.
+constexpr int kAccumulatorRegisters = 64;
 
 int read_int(std::istringstream& in, const char* what) {
   long long value;
@@ -102,7 +103,7 @@ namespace {
 
 // Split the paths sharing one input block into groups whose output blocks fit
 // the accumulator budget.  Paths writing the same output block stay together.
-std::vector<Group> make_groups(const Spec& spec) {
+std::vector<Group> make_groups(const Spec& spec, int budget) {
   std::map<std::tuple<int, int, int>, std::vector<int>> by_input;
   std::vector<std::tuple<int, int, int>> key_order;
   for (int p = 0; p < (int)spec.paths.size(); ++p) {
@@ -130,7 +131,7 @@ std::vector<Group> make_groups(const Spec& spec) {
     for (const auto& b : sorted) {
       bool placed = false;
       for (auto& bin : bins) {
-        if (bin.first + b.second <= kMaxAccumulators) {
+        if (bin.first + b.second <= budget) {
           bin.first += b.second;
           bin.second.push_back(b);
           placed = true;
@@ -165,6 +166,10 @@ std::vector<Group> make_groups(const Spec& spec) {
 template <typename RangesOf>
 int assign_phases(std::vector<Group>& groups, RangesOf ranges_of) {
   std::vector<std::vector<std::pair<long, long>>> phase_ranges;
+  if (const char* e = std::getenv("LUNAEQ_AMD_SPLIT"); e && std::atoi(e)) {
+    for (size_t n = 0; n < groups.size(); ++n) groups[n].phase = (int)n;
+    return (int)groups.size();
+  }
   for (Group& g : groups) {
     auto mine = ranges_of(g);
     int phase = 0;
@@ -199,7 +204,11 @@ void build_schedule(Plan& plan) {
   const Spec& spec = plan.spec;
 
   // ---- forward ----
-  plan.fwd_groups = make_groups(spec);
+  // The forward splits an input block's paths when their accumulators exceed
+  // the register budget (halved for fp64, whose values take two registers);
+  // the backward keeps one group per input block, because split groups would
+  // have to accumulate their gx messages.
+  plan.fwd_groups = make_groups(spec, kAccumulatorRegisters / (spec.dtype_bits / 32));
   auto out_ranges = [](const Group& g) {
     std::vector<std::pair<long, long>> r;
     for (const auto& b : g.blocks) r.push_back({b.out_off, b.out_off + (long)g.channels * b.d3});
@@ -236,7 +245,7 @@ void build_schedule(Plan& plan) {
     if (s > 65535) fail("too many channel chunks for one launch");
 
   // ---- backward ----
-  plan.bwd_groups = plan.fwd_groups;
+  plan.bwd_groups = make_groups(spec, kAccumulatorRegisters);
   auto in_ranges = [](const Group& g) {
     return std::vector<std::pair<long, long>>{{g.x_off, g.x_off + (long)g.channels * g.d1}};
   };
@@ -269,6 +278,14 @@ void build_schedule(Plan& plan) {
   }
   plan.bwd_phases = bwd_phases;
   plan.bwd_phase_slots = slots;
+  // Two waves per workgroup: the two 64-channel chunks of a 128-channel group
+  // gather adjacent halves of the same x rows together.  (All slots of a node
+  // in one workgroup, or the slots of a node on consecutive workgroups, keep
+  // every input block's gathers live at once and measured slower.)
+  int limit = 2;
+  if (const char* e = std::getenv("LUNAEQ_AMD_WG")) limit = std::max(0, std::min(16, std::atoi(e)));
+  for (int s : plan.phase_slots) plan.fwd_block_waves.push_back(std::min(s, limit));
+  for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(std::min(s, limit));
   plan.gy_parts = parts;
   for (int s : slots)
     if (s > 65535) fail("too many channel chunks for one launch");
