@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <set>
 #include <sstream>
@@ -50,7 +51,10 @@ struct Code {
 struct Options {
   int fwd_prefetch = 1;  // edge-loop software pipelining depth (0 none, 1 x/w, 2 all operands)
   int bwd_prefetch = 2;
-  int prefetch = 0;      // the depth of the kernel being emitted
+  int prefetch = 0;      // the level of the kernel being emitted
+  int fwd_depth = 1;     // edges in flight with prefetch level 2 (1 or 2)
+  int bwd_depth = 1;
+  int depth = 1;
   bool fwd_nt_w = true;  // stream the per-edge weights with non-temporal loads
   bool bwd_nt_w = false;
   bool nt_w = false;     // the setting of the kernel being emitted
@@ -76,6 +80,8 @@ Options options() {
     return at == std::string::npos ? fallback : std::atoi(s.c_str() + at + k.size());
   };
   o.fwd_prefetch = value("fpre", o.fwd_prefetch);
+  o.fwd_depth = value("fdepth", o.fwd_depth);
+  o.bwd_depth = value("bdepth", o.bwd_depth);
   o.fwd_nt_w = value("fntw", o.fwd_nt_w) != 0;
   o.bwd_nt_w = value("bntw", o.bwd_nt_w) != 0;
   o.nt_gw = value("ntgw", o.nt_gw) != 0;
@@ -237,12 +243,6 @@ std::vector<SignedClass> signed_classes(const std::map<std::pair<int, int>, std:
 }
 
 
-// Edge loop shared by the forward and backward groups.  With prefetch level 2
-// the operands of edge e+1 (x block, path weights, y row, env) and the source
-// index of edge e+2 are requested while edge e computes; empty asm statements
-// that read them at the end of the iteration make the wait for them land
-// there, after the iteration's stores, instead of at the loop head, where the
-// wait would also cover the stores just issued.
 // Emits the copy of y[yi] into a vector register before its first use.
 struct YCopies {
   bool on;
@@ -252,65 +252,76 @@ struct YCopies {
   }
 };
 
-void emit_operand_waits(Code& c, const Group& g, const GroupUse& use, bool env) {
-  for (int i = 0; i < g.d1; ++i) c.line("      asm volatile(\"\" :: \"v\"(nx%d));", i);
-  for (size_t n = 0; n < g.paths.size(); ++n) c.line("      asm volatile(\"\" :: \"v\"(nw%zu));", n);
-  for (int yi : use.ys) c.line("      asm volatile(\"\" :: \"s\"(ny%d));", yi);
-  if (env) c.line("      asm volatile(\"\" :: \"s\"(nev));");
-  c.line("      asm volatile(\"\" :: \"s\"(sn));");
-}
-
-void emit_loop_open(Code& c, const Spec& spec, const Group& g, const GroupUse& use, bool env,
-                    const Options& opt, const std::vector<std::string>& resident = {}) {
+// Edge loop shared by the forward and backward groups; `body` emits the work
+// of one edge e from x0.., w0.., y0.. and ev.
+//
+// prefetch 0: operands are loaded where they are used.
+// prefetch 1: the x block and the path weights of edge e+1 are requested
+//   while edge e computes.
+// prefetch 2: also the y row, env and (one further ahead) the source index.
+//   Empty asm statements that read the requested values at the end of the
+//   iteration make the wait for them land there, after the iteration's
+//   stores, instead of at the loop head, where it would also cover the stores
+//   just issued (vmcnt counts loads and stores in issue order).
+// depth 2 (with prefetch 2): two edges in flight, from two register buffers
+//   used alternately by a loop unrolled twice.
+void emit_edge_loop(Code& c, const Spec& spec, const Group& g, const GroupUse& use, bool env,
+                    const Options& opt, const std::vector<std::string>& resident,
+                    const std::function<void()>& body) {
   const int np = (int)g.paths.size();
-  auto load_edge = [&](const char* edge, const char* srcv) {
+  const bool full = opt.prefetch >= 2;
+  auto load_edge = [&](const char* edge, const char* srcv, char b) {
     c.line("      {");
     c.line("        const real* xq = x + (i64)%s * IN1 + (%d + uc * %d);", srcv, g.x_off, g.d1);
-    for (int i = 0; i < g.d1; ++i) c.line("        nx%d = xq[%d];", i, i);
+    for (int i = 0; i < g.d1; ++i) c.line("        %cx%d = xq[%d];", b, i, i);
     c.line("        const real* wq = w + (i64)%s * WNUM;", edge);
     for (int n = 0; n < np; ++n) {
       const Path& q = spec.paths[g.paths[n]];
       if (opt.nt_w)
-        c.line("        nw%d = __builtin_nontemporal_load(wq + %d + uc * %d);", n, q.w_off, q.w_stride);
+        c.line("        %cw%d = __builtin_nontemporal_load(wq + %d + uc * %d);", b, n, q.w_off, q.w_stride);
       else
-        c.line("        nw%d = wq[%d + uc * %d];", n, q.w_off, q.w_stride);
+        c.line("        %cw%d = wq[%d + uc * %d];", b, n, q.w_off, q.w_stride);
     }
-    if (opt.prefetch >= 2) {
+    if (full) {
       c.line("        const real* yq = y + (i64)%s * IN2;", edge);
-      for (int yi : use.ys) c.line("        ny%d = yq[%d];", yi, yi);
-      if (env) c.line("        nev = env[%s];", edge);
+      for (int yi : use.ys) c.line("        %cy%d = yq[%d];", b, yi, yi);
+      if (env) c.line("        %cev = env[%s];", b, edge);
     }
     c.line("      }");
   };
-  if (opt.prefetch >= 1) {
-    c.line("    if (beg < end) {");
-    for (int i = 0; i < g.d1; ++i) c.line("      real nx%d;", i);
-    for (int n = 0; n < np; ++n) c.line("      real nw%d;", n);
-    if (opt.prefetch >= 2) {
-      for (int yi : use.ys) c.line("      real ny%d;", yi);
-      if (env) c.line("      real nev;");
+  auto declare = [&](char b) {
+    for (int i = 0; i < g.d1; ++i) c.line("      real %cx%d;", b, i);
+    for (int n = 0; n < np; ++n) c.line("      real %cw%d;", b, n);
+    if (full) {
+      for (int yi : use.ys) c.line("      real %cy%d;", b, yi);
+      if (env) c.line("      real %cev;", b);
     }
-    c.line("      int sn = src[beg];");
-    load_edge("beg", "sn");
-    if (opt.prefetch >= 2) {
-      c.line("      sn = src[beg + 1 < end ? beg + 1 : beg];");
-      // Resolve the first edge's operands before the loop too, so that the
-      // loop head needs no wait on either incoming path.
-      emit_operand_waits(c, g, use, env);
-      for (const auto& name : resident) c.line("      asm volatile(\"\" :: \"v\"(%s));", name.c_str());
+  };
+  auto bind = [&](char b) {
+    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = %cx%d;", i, b, i);
+    for (int n = 0; n < np; ++n) c.line("      const real w%d = %cw%d;", n, b, n);
+    if (full) {
+      for (int yi : use.ys) c.line("      real y%d = %cy%d;", yi, b, yi);
+      if (env) c.line("      const real ev = %cev;", b);
     }
-    c.line("      for (int e = beg; e < end; ++e) {");
-    for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = nx%d;", i, i);
-    for (int n = 0; n < np; ++n) c.line("      const real w%d = nw%d;", n, n);
-    if (opt.prefetch >= 2) {
-      for (int yi : use.ys) c.line("      real y%d = ny%d;", yi, yi);
-      if (env) c.line("      const real ev = nev;");
-    }
-    c.line("      const int en = e + 1 < end ? e + 1 : e;");
-    if (opt.prefetch < 2) c.line("      sn = src[en];");
-    load_edge("en", "sn");
-    if (opt.prefetch >= 2) c.line("      sn = src[en + 1 < end ? en + 1 : en];");
-  } else {
+  };
+  auto waits = [&](char b) {
+    for (int i = 0; i < g.d1; ++i) c.line("      asm volatile(\"\" :: \"v\"(%cx%d));", b, i);
+    for (int n = 0; n < np; ++n) c.line("      asm volatile(\"\" :: \"v\"(%cw%d));", b, n);
+    for (int yi : use.ys) c.line("      asm volatile(\"\" :: \"s\"(%cy%d));", b, yi);
+    if (env) c.line("      asm volatile(\"\" :: \"s\"(%cev));", b);
+    c.line("      asm volatile(\"\" :: \"s\"(sn));");
+  };
+  auto inline_y = [&]() {
+    c.line("      const real* yr = y + (i64)e * IN2;");
+    for (int yi : use.ys) c.line("      real y%d = yr[%d];", yi, yi);
+    if (env) c.line("      const real ev = env[e];");
+  };
+  auto resident_waits = [&]() {
+    for (const auto& name : resident) c.line("      asm volatile(\"\" :: \"v\"(%s));", name.c_str());
+  };
+
+  if (opt.prefetch == 0) {
     c.line("    {");
     c.line("      for (int e = beg; e < end; ++e) {");
     c.line("      const int s = src[e];");
@@ -321,18 +332,74 @@ void emit_loop_open(Code& c, const Spec& spec, const Group& g, const GroupUse& u
       const Path& q = spec.paths[g.paths[n]];
       c.line("      const real w%d = wr[%d + uc * %d];", n, q.w_off, q.w_stride);
     }
+    inline_y();
+    body();
+    c.line("      }");
+    c.line("    }");
+    return;
   }
-  if (opt.prefetch < 2) {
-    c.line("      const real* yr = y + (i64)e * IN2;");
-    for (int yi : use.ys) c.line("      real y%d = yr[%d];", yi, yi);
-    if (env) c.line("      const real ev = env[e];");
+  c.line("    if (beg < end) {");
+  declare('n');
+  if (!full) {
+    c.line("      int sn = src[beg];");
+    load_edge("beg", "sn", 'n');
+    c.line("      for (int e = beg; e < end; ++e) {");
+    bind('n');
+    c.line("      const int en = e + 1 < end ? e + 1 : e;");
+    c.line("      sn = src[en];");
+    load_edge("en", "sn", 'n');
+    inline_y();
+    body();
+    c.line("      }");
+    c.line("    }");
+    return;
   }
-}
-
-void emit_loop_close(Code& c, const Spec& spec, const Group& g, const GroupUse& use, bool env,
-                     const Options& opt) {
-  (void)spec;
-  if (opt.prefetch >= 2) emit_operand_waits(c, g, use, env);
+  if (opt.depth < 2) {
+    c.line("      int sn = src[beg];");
+    load_edge("beg", "sn", 'n');
+    c.line("      sn = src[beg + 1 < end ? beg + 1 : beg];");
+    // Resolve the first edge's operands before the loop too, so that the loop
+    // head needs no wait on either incoming path.
+    waits('n');
+    resident_waits();
+    c.line("      for (int e = beg; e < end; ++e) {");
+    bind('n');
+    c.line("      const int en = e + 1 < end ? e + 1 : e;");
+    load_edge("en", "sn", 'n');
+    c.line("      sn = src[en + 1 < end ? en + 1 : en];");
+    body();
+    waits('n');
+    c.line("      }");
+    c.line("    }");
+    return;
+  }
+  // Two edges in flight: buffer n holds edge e (resolved), buffer m edge e+1.
+  declare('m');
+  c.line("      const int last = end - 1;");
+  c.line("      int sn = src[beg];");
+  load_edge("beg", "sn", 'n');
+  c.line("      sn = src[beg + 1 < end ? beg + 1 : last];");
+  load_edge("(beg + 1 < end ? beg + 1 : last)", "sn", 'm');
+  c.line("      sn = src[beg + 2 < end ? beg + 2 : last];");
+  waits('n');
+  resident_waits();
+  c.line("      for (int e0 = beg; e0 < end; e0 += 2) {");
+  for (int half = 0; half < 2; ++half) {
+    const char cur = half == 0 ? 'n' : 'm', other = half == 0 ? 'm' : 'n';
+    if (half == 0)
+      c.line("      {");
+    else
+      c.line("      if (e0 + 1 < end) {");
+    c.line("      const int e = e0 + %d;", half);
+    bind(cur);
+    // Refill this buffer with edge e+2 and fetch the source index of e+3.
+    c.line("      const int en = e + 2 < end ? e + 2 : last;");
+    load_edge("en", "sn", cur);
+    c.line("      sn = src[en + 1 < end ? en + 1 : last];");
+    body();
+    waits(other);
+    c.line("      }");
+  }
   c.line("      }");
   c.line("    }");
 }
@@ -346,7 +413,7 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
   c.line("    const int uc = active ? u : %d;", g.channels - 1);
   for (size_t b = 0; b < g.blocks.size(); ++b)
     for (int k = 0; k < g.blocks[b].d3; ++k) c.line("    real A%zu_%d = 0;", b, k);
-  emit_loop_open(c, spec, g, use, env, opt);
+  auto body = [&]() {
   // l0 columns are summed over the paths (edge copies) sharing them.
   std::map<int, std::vector<int>> l0_cols;
   for (int n = 0; n < np; ++n) {
@@ -420,7 +487,8 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
   }
   for (const auto& col : l0_cols)
     c.line("      l0[(i64)e * L0DIM + %d + uc] = L%d;", col.first, col.first);
-  emit_loop_close(c, spec, g, use, env, opt);
+  };
+  emit_edge_loop(c, spec, g, use, env, opt, {}, body);
   c.line("    if (active) {");
   for (size_t b = 0; b < g.blocks.size(); ++b) {
     const AccBlock& blk = g.blocks[b];
@@ -439,12 +507,17 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
 // group in registers and streams the node's in-edges, writing gw and the gy
 // partials per edge and the per-edge gx message msg[e, x block]; a second
 // kernel sums the messages over each source node's out-edges.
-void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
-                         bool want_msg, bool want_part, const Options& opt) {
+// One wave's share of a backward group: all of its paths, or one subset of
+// a split group (`g` is then the subset's view, sub its index).
+void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
+                        bool want_msg, bool want_part, const Options& opt, int sub) {
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
   const int np = (int)g.paths.size();
-  c.line("    const int u = (slot - %d) * 64 + lane;", g.slot_base);
+  if (g.subsets > 1)
+    c.line("    const int u = ((slot - %d) / %d) * 64 + lane;", g.slot_base, g.subsets);
+  else
+    c.line("    const int u = (slot - %d) * 64 + lane;", g.slot_base);
   c.line("    const bool active = u < %d;", g.channels);
   c.line("    const int uc = active ? u : %d;", g.channels - 1);
   std::vector<std::string> seeds;
@@ -456,7 +529,7 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
       seeds.push_back("G" + std::to_string(b) + "_" + std::to_string(k));
     }
   }
-  emit_loop_open(c, spec, g, use, env, opt, seeds);
+  auto body = [&]() {
   if (!opt.hoist) {
     // Opaque to the optimiser: keeps the edge-invariant q_ij inside the loop
     // instead of holding all of them in registers across it.
@@ -577,7 +650,21 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
     for (int i : is) c.line("        M%d = FMA(ws, a%d, M%d);", i, i, i);
     c.line("      }");
   }
-  if (want_msg) {
+  if (want_msg && g.subsets > 1) {
+    // The second subset hands its message share to the first through LDS
+    // (two buffers by edge parity: one barrier per edge orders both uses).
+    c.line("      {");
+    c.line("        const int par = (e - beg) & 1;");
+    if (sub == 1) {
+      for (int i = 0; i < g.d1; ++i) c.line("        msg_share[par][%d][lane] = M%d;", i, i);
+      c.line("        __syncthreads();");
+    } else {
+      c.line("        __syncthreads();");
+      for (int i = 0; i < g.d1; ++i) c.line("        M%d += msg_share[par][%d][lane];", i, i);
+    }
+    c.line("      }");
+  }
+  if (want_msg && sub == 0) {
     // Lanes past the last channel repeat channel C-1 exactly, so their stores
     // write identical values; only the cross-lane sums below must mask them.
     c.line("      {");
@@ -596,7 +683,42 @@ void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bo
   for (int yi : use.ys) values.push_back("GY" + std::to_string(yi));
   if (env) values.push_back("GE");
   flush(values);
-  emit_loop_close(c, spec, g, use, env, opt);
+  };
+  emit_edge_loop(c, spec, g, use, env, opt, seeds, body);
+}
+
+// The paths of subset `sub` of a split group, as a group of their own.
+Group subset_view(const Group& g, int sub) {
+  Group view = g;
+  view.paths.clear();
+  view.path_block.clear();
+  view.blocks.clear();
+  std::map<int, int> remap;
+  for (size_t n = 0; n < g.paths.size(); ++n) {
+    if (g.path_subset[n] != sub) continue;
+    const int b = g.path_block[n];
+    if (!remap.count(b)) {
+      remap[b] = (int)view.blocks.size();
+      view.blocks.push_back(g.blocks[b]);
+    }
+    view.paths.push_back(g.paths[n]);
+    view.path_block.push_back(remap[b]);
+  }
+  return view;
+}
+
+void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
+                         bool want_msg, bool want_part, const Options& opt) {
+  if (g.subsets == 1) {
+    emit_backward_wave(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt, 0);
+    return;
+  }
+  c.line("    const int sub = (slot - %d) %% %d;", g.slot_base, g.subsets);
+  for (int sub = 0; sub < g.subsets; ++sub) {
+    c.line("    %sif (sub == %d) {", sub ? "else " : "", sub);
+    emit_backward_wave(c, spec, subset_view(g, sub), env, gl0, want_gw, want_msg, want_part, opt, sub);
+    c.line("    }");
+  }
 }
 
 std::string kernel_attributes(int wpe) {
@@ -610,6 +732,7 @@ std::string emit_forward(const Plan& plan, bool env, bool l0) {
   const Spec& spec = plan.spec;
   Options opt = options();
   opt.prefetch = opt.fwd_prefetch;
+  opt.depth = opt.fwd_depth;
   opt.nt_w = opt.fwd_nt_w;
   if (opt.fwd_local < 0) opt.fwd_local = spec.dtype_bits == 64;
   Code c;
@@ -625,7 +748,9 @@ std::string emit_forward(const Plan& plan, bool env, bool l0) {
       // One wave per workgroup, the slots of a node on consecutive workgroups.
       c.line("  const int lane = threadIdx.x;");
       c.line("  const int t = order[blockIdx.x / %d];", slots);
-      c.line("  const int slot = blockIdx.x %% %d;", slots);
+      // Rotated per node, so that the slots spread evenly over the XCDs
+      // (workgroups go to XCDs round-robin).
+      c.line("  const int slot = (blockIdx.x + blockIdx.x / %d) %% %d;", slots, slots);
     } else {
       c.line("  const int lane = threadIdx.x & 63;");
       c.line("  const int t = order[blockIdx.x];");
@@ -650,6 +775,7 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   const Spec& spec = plan.spec;
   Options opt = options();
   opt.prefetch = opt.bwd_prefetch;
+  opt.depth = opt.bwd_depth;
   opt.nt_w = opt.bwd_nt_w;
   Code c;
   c.raw(prelude(spec));
@@ -661,11 +787,17 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     c.line("    const real* __restrict__ env, const real* __restrict__ g, const real* __restrict__ gl0,");
     c.line("    const int* __restrict__ src, const int* __restrict__ rowptr, const int* __restrict__ order,");
     c.line("    real* __restrict__ gw, real* __restrict__ msg, real* __restrict__ part, i64 E) {");
+    int share_d1 = 0;
+    for (const Group& g : plan.bwd_groups)
+      if (g.phase == phase && g.subsets > 1) share_d1 = std::max(share_d1, g.d1);
+    if (share_d1 > 0 && want_msg) c.line("  __shared__ real msg_share[2][%d][64];", share_d1);
     if (waves == 0) {
       // One wave per workgroup, the slots of a node on consecutive workgroups.
       c.line("  const int lane = threadIdx.x;");
       c.line("  const int t = order[blockIdx.x / %d];", slots);
-      c.line("  const int slot = blockIdx.x %% %d;", slots);
+      // Rotated per node, so that the slots spread evenly over the XCDs
+      // (workgroups go to XCDs round-robin).
+      c.line("  const int slot = (blockIdx.x + blockIdx.x / %d) %% %d;", slots, slots);
     } else {
       c.line("  const int lane = threadIdx.x & 63;");
       c.line("  const int t = order[blockIdx.x];");
@@ -676,7 +808,9 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     bool first = true;
     for (const Group& g : plan.bwd_groups) {
       if (g.phase != phase) continue;
-      c.line("  %sif (slot < %d) {", first ? "" : "else ", g.slot_base + g.chunks);
+      // A split group may start after an unused (padding) slot: test both ends.
+      c.line("  %sif (slot >= %d && slot < %d) {", first ? "" : "else ", g.slot_base,
+             g.slot_base + g.chunks * g.subsets);
       first = false;
       emit_backward_group(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt);
       c.line("  }");
@@ -688,11 +822,14 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   const int pw = spec.in2 + (env ? 1 : 0);
   std::vector<std::vector<std::pair<int, int>>> writers(pw);
   for (const Group& g : plan.bwd_groups) {
-    GroupUse use = group_use(spec, g);
-    for (int chunk = 0; chunk < g.chunks; ++chunk) {
-      int col = 0;
-      for (int yi : use.ys) writers[yi].push_back({g.gy_slot_base + chunk, col++});
-      if (env) writers[spec.in2].push_back({g.gy_slot_base + chunk, col});
+    for (int sub = 0; sub < g.subsets; ++sub) {
+      GroupUse use = group_use(spec, g.subsets > 1 ? subset_view(g, sub) : g);
+      for (int chunk = 0; chunk < g.chunks; ++chunk) {
+        const int slot = g.gy_slot_base + chunk * g.subsets + sub;
+        int col = 0;
+        for (int yi : use.ys) writers[yi].push_back({slot, col++});
+        if (env) writers[spec.in2].push_back({slot, col});
+      }
     }
   }
   // One thread per edge; every output column is a fixed sum of partial columns.

@@ -24,6 +24,8 @@ constexpr int kWave = 64;
 // Upper bound on live output accumulators per lane for one group.
 // Accumulator budget per wave, in 32-bit registers.
 constexpr int kAccumulatorRegisters = 64;
+// fp64 backward groups holding more seeds than this are split in two.
+constexpr int kSplitSeeds = 24;
 
 int read_int(std::istringstream& in, const char* what) {
   long long value;
@@ -166,10 +168,6 @@ std::vector<Group> make_groups(const Spec& spec, int budget) {
 template <typename RangesOf>
 int assign_phases(std::vector<Group>& groups, RangesOf ranges_of) {
   std::vector<std::vector<std::pair<long, long>>> phase_ranges;
-  if (const char* e = std::getenv("LUNAEQ_AMD_SPLIT"); e && std::atoi(e)) {
-    for (size_t n = 0; n < groups.size(); ++n) groups[n].phase = (int)n;
-    return (int)groups.size();
-  }
   for (Group& g : groups) {
     auto mine = ranges_of(g);
     int phase = 0;
@@ -266,15 +264,44 @@ void build_schedule(Plan& plan) {
   plan.bwd_gx_needs_zero = x_collision || x_holes;
   for (Group& g : plan.bwd_groups) g.gx_accumulate = x_collision;
   int bwd_phases = assign_phases(plan.bwd_groups, in_ranges);
-  // Backward phases reuse Group::phase; slots are numbered per phase, and
+  // fp64 groups with many seeds run as two path subsets (half the seeds in
+  // registers per wave, which doubles or triples the waves that fit).
+  int split_seeds = spec.dtype_bits == 64 ? kSplitSeeds : 0;
+  if (const char* e = std::getenv("LUNAEQ_AMD_BSPLIT")) split_seeds = std::atoi(e);
+  bool any_split = false;
+  for (Group& g : plan.bwd_groups) {
+    int seeds = 0;
+    for (const auto& b : g.blocks) seeds += b.d3;
+    g.path_subset.assign(g.paths.size(), 0);
+    if (split_seeds <= 0 || seeds <= split_seeds || g.paths.size() < 2) continue;
+    // Greedy balance of per-edge work: terms plus the seeds each path holds.
+    std::vector<int> order(g.paths.size());
+    for (size_t n = 0; n < order.size(); ++n) order[n] = (int)n;
+    auto cost = [&](int n) {
+      const Path& q = spec.paths[g.paths[n]];
+      return (long)q.terms.size() + 2L * q.d3 + q.d1 + q.d2;
+    };
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return cost(a) > cost(b); });
+    long load[2] = {0, 0};
+    for (int n : order) {
+      const int s = load[1] < load[0] ? 1 : 0;
+      g.path_subset[n] = s;
+      load[s] += cost(n);
+    }
+    g.subsets = 2;
+    any_split = true;
+  }
+  // Backward phases reuse Group::phase; slots are numbered per phase (a split
+  // group starts on an even slot, so its waves pair up in one workgroup), and
   // gy partial slots are global.
   std::vector<int> slots(bwd_phases, 0);
   int parts = 0;
   for (Group& g : plan.bwd_groups) {
+    if (g.subsets > 1 && slots[g.phase] % 2) ++slots[g.phase];
     g.slot_base = slots[g.phase];
-    slots[g.phase] += g.chunks;
+    slots[g.phase] += g.chunks * g.subsets;
     g.gy_slot_base = parts;
-    parts += g.chunks;
+    parts += g.chunks * g.subsets;
   }
   plan.bwd_phases = bwd_phases;
   plan.bwd_phase_slots = slots;
@@ -285,7 +312,7 @@ void build_schedule(Plan& plan) {
   int limit = 2;
   if (const char* e = std::getenv("LUNAEQ_AMD_WG")) limit = std::max(0, std::min(16, std::atoi(e)));
   for (int s : plan.phase_slots) plan.fwd_block_waves.push_back(std::min(s, limit));
-  for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(std::min(s, limit));
+  for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(any_split ? 2 : std::min(s, limit));
   plan.gy_parts = parts;
   for (int s : slots)
     if (s > 65535) fail("too many channel chunks for one launch");

@@ -124,3 +124,14 @@ def test_product_path_has_no_cpu_fallback():
     x = torch.randn(2, conv.irreps_in1.dim)
     with pytest.raises(RuntimeError, match="GPU"):
         conv(x, torch.randn(2, conv.irreps_in2.dim), torch.randn(2, conv.weight_numel), graph=graph)
+
+
+def test_fp64_backward_splits_large_groups():
+    """fp64 backward groups holding more than 24 output seeds run as two path
+    subsets, each with its own gy partial slot per channel chunk; fp32 keeps one
+    wave per group and chunk."""
+    # lmax=3, 128 channels: input blocks l=0..3 hold 16, 39, 51, 50 seeds.
+    f32 = op_for(channels=128, lmax=3, dtype=torch.float32).plan.info
+    f64 = op_for(channels=128, lmax=3, dtype=torch.float64).plan.info
+    assert f32.gy_parts == 4 * 2
+    assert f64.gy_parts == 2 + 3 * 2 * 2
