@@ -158,12 +158,14 @@ int luna_uvw_plan_precompile(LunaUvwPlan* plan);
 int luna_uvw_fwd(const LunaUvwPlan* plan, const void* x, const void* y, const void* weight,
                  void* out, int64_t rows, LunaStream stream);
 
-/* Bytes of workspace luna_uvw_bwd needs when gw is requested. */
+/* Bytes of workspace luna_uvw_bwd needs (weight-gradient partials per 256-row
+ * chunk and edge-gradient partials per input block and 32-wide K tile). */
 int luna_uvw_bwd_workspace(const LunaUvwPlan* plan, int64_t rows, size_t* bytes);
 
 /*
  * Backward of luna_uvw_fwd for seed g [rows, out]: gx and gy (both or neither)
- * and gw [weight_numel] (NULL to skip; then workspace may be NULL).
+ * and gw [weight_numel] (NULL to skip).  workspace must hold
+ * luna_uvw_bwd_workspace bytes whenever anything is requested.
  * replaces: the UVW backward launcher (src/lunatp/uvw/interface.py:42-49)
  */
 int luna_uvw_bwd(const LunaUvwPlan* plan, const void* x, const void* y, const void* weight,

@@ -40,8 +40,7 @@ struct UvwSpec {
   std::vector<UvwPath> paths;
 };
 
-constexpr int kRows = 32;       // batch rows per workgroup tile
-constexpr int kChunkTiles = 8;  // row tiles per workgroup in the weight-gradient pass
+constexpr int kChunkRows = 256;  // batch rows per wave (and per partial) of the weight gradient
 
 int read_int(std::istringstream& in, const char* what) {
   long long value;
@@ -83,8 +82,8 @@ UvwSpec parse(const std::string& text) {
     if ((long)p.out_off + (long)p.mul3 * p.d3 > s.out) fail("uvw spec: output block outside out_dim");
     if ((long)p.w_off + (long)p.mul1 * p.mul2 * p.mul3 > s.wnum) fail("uvw spec: weights outside weight_numel");
     if (p.d3 > 16) fail("uvw spec: output degree above 7 is not supported");
-    if (p.mul1 * p.mul2 > 64 && 64 % p.mul2 != 0)
-      fail("uvw spec: edge multiplicity must divide 64 when mul1*mul2 exceeds 64");
+    // The backward sums over v inside a lane's runs of four consecutive K = (u, v).
+    if (4 % p.mul2 != 0) fail("uvw spec: edge multiplicity must be 1, 2 or 4");
     for (int t = 0; t < nterms; ++t) {
       UvwTerm term;
       term.i = read_int(in, "i");
@@ -123,41 +122,90 @@ std::string flit(double c) {
 
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
-// Output blocks in first-use order, with the paths feeding each.
-struct OutBlock {
-  int out_off, mul3, d3;
+bool overlap(long a0, long a1, long b0, long b1) { return a0 < b1 && b0 < a1; }
+
+// A launch unit: a set of paths whose results one wave combines in registers.
+//   forward:  paths writing one output block (out_off, mul3, d3)
+//   backward: paths reading one input block (x_off, mul1, d1) with one mul2
+struct Unit {
   std::vector<int> paths;
+  long lo = 0, hi = 0;  // element range written (out for forward, gx for backward)
+  int phase = 0;
+  bool accumulate = false;
+  int slot_base = 0;    // backward: first gy partial slot (one per K tile)
 };
 
-std::vector<OutBlock> out_blocks(const UvwSpec& s) {
-  std::vector<OutBlock> blocks;
+// Units of each phase write disjoint ranges; when ranges of different units
+// overlap at all, every unit accumulates into a zero-filled output.
+int assign_phases(std::vector<Unit>& units, bool* collision) {
+  *collision = false;
+  for (size_t a = 0; a < units.size(); ++a)
+    for (size_t b = a + 1; b < units.size(); ++b)
+      if (overlap(units[a].lo, units[a].hi, units[b].lo, units[b].hi)) *collision = true;
+  std::vector<std::vector<std::pair<long, long>>> taken;
+  for (Unit& u : units) {
+    u.accumulate = *collision;
+    int phase = 0;
+    for (;; ++phase) {
+      if (phase == (int)taken.size()) taken.emplace_back();
+      bool clash = false;
+      for (const auto& r : taken[phase]) clash = clash || overlap(u.lo, u.hi, r.first, r.second);
+      if (!clash) break;
+    }
+    u.phase = phase;
+    taken[phase].push_back({u.lo, u.hi});
+  }
+  return (int)taken.size();
+}
+
+std::vector<Unit> forward_units(const UvwSpec& s) {
+  std::vector<Unit> units;
   for (int p = 0; p < (int)s.paths.size(); ++p) {
     const UvwPath& q = s.paths[p];
     bool found = false;
-    for (auto& b : blocks)
-      if (b.out_off == q.out_off && b.mul3 == q.mul3 && b.d3 == q.d3) {
-        b.paths.push_back(p);
+    for (Unit& u : units) {
+      const UvwPath& r = s.paths[u.paths[0]];
+      if (r.out_off == q.out_off && r.mul3 == q.mul3 && r.d3 == q.d3) {
+        u.paths.push_back(p);
         found = true;
+        break;
       }
-    if (!found) blocks.push_back({q.out_off, q.mul3, q.d3, {p}});
+    }
+    if (!found) units.push_back({{p}, q.out_off, q.out_off + (long)q.mul3 * q.d3});
   }
-  return blocks;
+  return units;
 }
 
-struct Dims {
-  int kt;      // K tile (multiple of 8: two halves of s-steps, 4 at a time)
-  int npad;    // output channels rounded up to 32
-  int d3max;
-};
-
-Dims dims(const UvwSpec& s) {
-  Dims d{0, 0, 0};
-  for (const auto& p : s.paths) {
-    d.npad = std::max(d.npad, round_up(p.mul3, 32));
-    d.d3max = std::max(d.d3max, p.d3);
+std::vector<Unit> backward_units(const UvwSpec& s) {
+  std::vector<Unit> units;
+  for (int p = 0; p < (int)s.paths.size(); ++p) {
+    const UvwPath& q = s.paths[p];
+    bool found = false;
+    for (Unit& u : units) {
+      const UvwPath& r = s.paths[u.paths[0]];
+      if (r.x_off == q.x_off && r.mul1 == q.mul1 && r.d1 == q.d1 && r.mul2 == q.mul2) {
+        u.paths.push_back(p);
+        found = true;
+        break;
+      }
+    }
+    if (!found) units.push_back({{p}, q.x_off, q.x_off + (long)q.mul1 * q.d1});
   }
-  d.kt = 64;
-  return d;
+  return units;
+}
+
+int ktiles(const UvwPath& q) { return (q.mul1 * q.mul2 + 31) / 32; }
+
+// Sorted distinct (i) and (j) indices of a path's terms.
+std::set<int> term_is(const UvwPath& q) {
+  std::set<int> r;
+  for (const auto& t : q.terms) r.insert(t.i);
+  return r;
+}
+std::set<int> term_js(const UvwPath& q) {
+  std::set<int> r;
+  for (const auto& t : q.terms) r.insert(t.j);
+  return r;
 }
 
 const char* kPrelude = R"(
@@ -165,365 +213,358 @@ typedef float real;
 typedef long long i64;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 #define FMA(a, b, c) __builtin_fmaf((a), (b), (c))
+// D[i][j] += sum_{k<2} A[i][k] B[k][j]; lane l supplies A[l%32][l/32] and
+// B[l/32][l%32]; register r of lane l holds D[8(r/4) + 4(l/32) + r%4][l%32].
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 )";
 
-// Emits the CG producer for one (row, K) pair of path q: z0..z{d3-1}.
-void emit_producer(Code& c, const UvwSpec& s, const UvwPath& q, const char* row, const char* kvar, const char* ind) {
-  c.line("%sconst int pu = %s / %d, pv = %s - (%s / %d) * %d;", ind, kvar, q.mul2, kvar, kvar, q.mul2, q.mul2);
-  c.line("%sconst real* xq = x + (i64)%s * %d + %d + pu * %d;", ind, row, s.in1, q.x_off, q.d1);
-  c.line("%sconst real* yq = y + (i64)%s * %d + %d + pv * %d;", ind, row, s.in2, q.y_off, q.d2);
-  std::set<int> is, js;
-  for (const auto& t : q.terms) {
-    is.insert(t.i);
-    js.insert(t.j);
-  }
-  for (int i : is) c.line("%sconst real px%d = xq[%d];", ind, i, i);
-  for (int j : js) c.line("%sconst real py%d = yq[%d];", ind, j, j);
-  for (int k = 0; k < q.d3; ++k) c.line("%sreal z%d = 0;", ind, k);
-  for (const auto& t : q.terms)
-    c.line("%sz%d = FMA(%s, px%d * py%d, z%d);", ind, t.k, flit(t.c).c_str(), t.i, t.j, t.k);
+// Common head of every kernel: four independent waves per workgroup.
+void emit_head(Code& c) {
+  c.line("  const int lane = threadIdx.x & 63, hk = lane >> 5, col = lane & 31;");
+  c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
 }
 
 // ---------------------------------------------------------------- forward
-std::string emit_forward(const UvwSpec& s) {
-  const Dims d = dims(s);
-  const int ZW = d.kt + 4;  // padded row of the LDS tiles (keeps 16-byte alignment)
+// out^T[w, b] = sum_p sum_K W_p[K, w] Z_p[b, K] per output component k, on
+// the matrix cores with A = W_p^T (rows w, 32 output channels per wave), B =
+// Z_p (32 batch rows per wave), K = (u, v) two per instruction.  Each lane
+// produces its own B operand, Z_p[b0 + col, K = 2s + hk, k] for every k, from
+// the x and y rows of its batch row (the sparse CG terms as VALU work).
+std::string emit_forward(const UvwSpec& s, const std::vector<Unit>& units, int phases) {
   Code c;
   c.s << kPrelude;
-  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_fwd(");
-  c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
-  c.line("    real* __restrict__ out, int B) {");
-  c.line("  __shared__ __attribute__((aligned(16))) real zs[%d][%d][%d];", d.d3max, kRows, ZW);
-  c.line("  __shared__ __attribute__((aligned(16))) real ws[%d][%d];", d.npad, ZW);
-  c.line("  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;");
-  c.line("  const int b0 = blockIdx.x * %d;", kRows);
-  c.line("  const int half = lane >> 5, col = lane & 31;");
-  for (const OutBlock& blk : out_blocks(s)) {
-    const int nt = round_up(blk.mul3, 32) / 32;
-    const int tiles = blk.d3 * nt;
-    const int per_wave = (tiles + 3) / 4;
-    c.line("  {");
-    c.line("    floatx16 acc[%d];", per_wave);
-    c.line("    for (int t = 0; t < %d; ++t) acc[t] = (floatx16)(0.0f);", per_wave);
-    for (int p : blk.paths) {
-      const UvwPath& q = s.paths[p];
-      const int K = q.mul1 * q.mul2;
-      for (int k0 = 0; k0 < K; k0 += d.kt) {
-        c.line("    __syncthreads();");
-        // Stage Z tile: kRows x kt pairs (b, K).
-        c.line("    for (int idx = tid; idx < %d; idx += 256) {", kRows * d.kt);
-        c.line("      const int kk = idx %% %d, b = idx / %d, kg = %d + kk;", d.kt, d.kt, k0);
-        c.line("      const int row = b0 + b;");
-        c.line("      if (kg < %d && row < B) {", K);
-        emit_producer(c, s, q, "row", "kg", "        ");
-        for (int k = 0; k < q.d3; ++k) c.line("        zs[%d][b][kk] = z%d;", k, k);
-        c.line("      } else {");
-        for (int k = 0; k < q.d3; ++k) c.line("        zs[%d][b][kk] = 0;", k);
+  for (int phase = 0; phase < phases; ++phase) {
+    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_fwd_p%d(", phase);
+    c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
+    c.line("    real* __restrict__ out, int B) {");
+    emit_head(c);
+    c.line("  const int b0 = (blockIdx.x * 4 + wave) * 32;");
+    c.line("  if (b0 >= B) return;");
+    c.line("  const int brow = b0 + col < B ? b0 + col : B - 1;");
+    c.line("  int unit = blockIdx.y;");
+    for (const Unit& u : units) {
+      if (u.phase != phase) continue;
+      const UvwPath& head = s.paths[u.paths[0]];
+      const int d3 = head.d3, mul3 = head.mul3;
+      const int nt = (mul3 + 31) / 32;
+      c.line("  if (unit < %d) {", nt);
+      c.line("    const int w0 = unit * 32;");
+      for (int k = 0; k < d3; ++k) c.line("    floatx16 acc%d = (floatx16)(0.0f);", k);
+      c.line("    const bool wok = w0 + col < %d;", mul3);
+      for (int p : u.paths) {
+        const UvwPath& q = s.paths[p];
+        const int K = q.mul1 * q.mul2;
+        const std::set<int> is = term_is(q), js = term_js(q);
+        c.line("    {");
+        c.line("      const real* xr = x + (i64)brow * %d + %d;", s.in1, q.x_off);
+        c.line("      const real* yr = y + (i64)brow * %d + %d;", s.in2, q.y_off);
+        c.line("      const real* wr = wt + %d + (wok ? w0 + col : 0);", q.w_off);
+        if (q.mul2 == 1)
+          for (int j : js) c.line("      const real y%d = yr[%d];", j, j);
+        c.line("      #pragma unroll 4");
+        c.line("      for (int s = 0; s < %d; ++s) {", (K + 1) / 2);
+        // An odd K leaves the last upper-half lane without a pair: its A is
+        // zero and its loads use the last valid pair.
+        c.line("        const int kk = 2 * s + hk;");
+        c.line("        const bool kok = kk < %d;", K);
+        c.line("        const int kc = kok ? kk : %d;", K - 1);
+        c.line("        const int u = kc / %d, v = kc %% %d;", q.mul2, q.mul2);
+        c.line("        (void)v;");
+        for (int i : is) c.line("        const real x%d = xr[u * %d + %d];", i, q.d1, i);
+        if (q.mul2 != 1)
+          for (int j : js) c.line("        const real y%d = yr[v * %d + %d];", j, q.d2, j);
+        c.line("        const real a = (kok && wok) ? wr[(i64)kc * %d] : 0.0f;", mul3);
+        for (int k = 0; k < d3; ++k) c.line("        real z%d = 0;", k);
+        for (const auto& t : q.terms)
+          c.line("        z%d = FMA(%s, x%d * y%d, z%d);", t.k, flit(t.c).c_str(), t.i, t.j, t.k);
+        for (int k = 0; k < d3; ++k) c.line("        acc%d = mfma32(a, z%d, acc%d);", k, k, k);
         c.line("      }");
         c.line("    }");
-        // Stage W transposed: ws[n][kk] = W[k0 + kk, n].
-        c.line("    for (int idx = tid; idx < %d; idx += 256) {", d.kt * d.npad);
-        c.line("      const int n = idx %% %d, kk = idx / %d, kg = %d + kk;", d.npad, d.npad, k0);
-        c.line("      ws[n][kk] = (kg < %d && n < %d) ? wt[%d + (i64)kg * %d + n] : 0.0f;", K, q.mul3, q.w_off,
-               q.mul3);
-        c.line("    }");
-        c.line("    __syncthreads();");
-        // Matrix-core contraction over this K tile.
-        for (int t = 0; t < tiles; ++t) {
-          const int owner = t % 4, slot = t / 4, k = t / nt, n0 = (t % nt) * 32;
-          c.line("    if (wave == %d) {", owner);
-          c.line("      floatx16 a_acc = acc[%d];", slot);
-          c.line("      for (int s = 0; s < %d; s += 4) {", d.kt / 2);
-          c.line("        const float4 av = *(const float4*)&zs[%d][col][half * %d + s];", k, d.kt / 2);
-          c.line("        const float4 bv = *(const float4*)&ws[%d + col][half * %d + s];", n0, d.kt / 2);
-          c.line("        a_acc = mfma32(av.x, bv.x, a_acc);");
-          c.line("        a_acc = mfma32(av.y, bv.y, a_acc);");
-          c.line("        a_acc = mfma32(av.z, bv.z, a_acc);");
-          c.line("        a_acc = mfma32(av.w, bv.w, a_acc);");
-          c.line("      }");
-          c.line("      acc[%d] = a_acc;", slot);
-          c.line("    }");
-        }
       }
-    }
-    // Store: acc register r of lane holds row 8*(r/4) + 4*half + r%4, channel n0 + col.
-    for (int t = 0; t < tiles; ++t) {
-      const int owner = t % 4, slot = t / 4, k = t / nt, n0 = (t % nt) * 32;
-      c.line("    if (wave == %d && %d + col < %d) {", owner, n0, blk.mul3);
+      // Register r: output channel w0 + 8(r/4) + 4hk + r%4 of batch row b0 + col.
+      c.line("    if (b0 + col < B) {");
+      c.line("      real* orow = out + (i64)(b0 + col) * %d + %d;", s.out, head.out_off);
+      c.line("      #pragma unroll");
       c.line("      for (int r = 0; r < 16; ++r) {");
-      c.line("        const int row = b0 + 8 * (r >> 2) + 4 * half + (r & 3);");
-      c.line("        if (row < B) out[(i64)row * %d + %d + (%d + col) * %d + %d] = acc[%d][r];", s.out, blk.out_off,
-             n0, blk.d3, k, slot);
+      c.line("        const int w = w0 + 8 * (r >> 2) + 4 * hk + (r & 3);");
+      c.line("        if (w < %d) {", mul3);
+      for (int k = 0; k < d3; ++k)
+        c.line("          orow[w * %d + %d] %s acc%d[r];", d3, k, u.accumulate ? "+=" : "=", k);
+      c.line("        }");
       c.line("      }");
       c.line("    }");
+      c.line("    return;");
+      c.line("  }");
+      c.line("  unit -= %d;", nt);
     }
-    c.line("  }");
+    c.line("}");
   }
-  c.line("}");
   return c.s.str();
 }
 
-// Store mode of every gx tile in emission order ('S' first write, 'A'
-// accumulate).  Tiles of paths that share an input block but split it into
-// different channel ranges make first writes ambiguous; then every tile
-// accumulates and the caller zero-fills gx.
-std::vector<char> gx_modes(const UvwSpec& s, bool* all_accumulate) {
-  const Dims d = dims(s);
-  std::map<int, std::vector<char>> touched;  // x_off -> per-u flag
-  std::vector<std::pair<int, std::pair<int, int>>> tiles;  // (x_off, [u0, u1))
-  for (const OutBlock& blk : out_blocks(s))
-    for (int p : blk.paths) {
-      const UvwPath& q = s.paths[p];
-      const int K = q.mul1 * q.mul2;
-      for (int k0 = 0; k0 < K; k0 += d.kt) {
-        const int ku = std::min(d.kt, K - k0);
-        tiles.push_back({q.x_off, {k0 / q.mul2, (k0 + ku + q.mul2 - 1) / q.mul2}});
-      }
-    }
-  std::vector<char> modes;
-  bool mixed = false;
-  for (const auto& t : tiles) {
-    const UvwPath* owner = nullptr;
-    for (const auto& q : s.paths)
-      if (q.x_off == t.first) owner = &q;
-    auto& flags = touched[t.first];
-    if (flags.empty()) flags.assign(owner->mul1, 0);
-    int count = 0;
-    for (int u = t.second.first; u < t.second.second; ++u) count += flags[u];
-    const int width = t.second.second - t.second.first;
-    if (count != 0 && count != width) mixed = true;
-    modes.push_back(count == 0 ? 'S' : 'A');
-    for (int u = t.second.first; u < t.second.second; ++u) flags[u] = 1;
-  }
-  if (mixed)
-    for (char& m : modes) m = 'A';
-  *all_accumulate = mixed;
-  return modes;
-}
-
 // ---------------------------------------------------------------- backward: gx, gy
-std::string emit_backward_xy(const UvwSpec& s) {
-  const Dims d = dims(s);
-  const int GW = d.npad + 4;  // padded rows of the g tile
-  const int ZW = d.kt + 4;
+// dZ_p^T[K, b] = sum_w W_p[K, w] g[b, oo + w*d3 + k] on the matrix cores with
+// v_mfma_f32_16x16x4f32 (A = W_p, 16 K indices per wave; B = the seed rows of
+// 16 batch rows; contraction over w, four per instruction).  Lane l then
+// holds dZ for batch row b0 + l%16 and the four consecutive K indices
+// 16 kt + 4(l/16) + r, so both contractions with the CG terms stay in the lane:
+//   gx[b, u, i] += sum_{v,j,k} c y[b, v, j] dZ[b, k, (u, v)]   (v summed in-lane: mul2 | 4)
+//   gy[b, v, j] += sum_{u,i,k} c x[b, u, i] dZ[b, k, (u, v)]   (then summed over the
+//                                                             four lane groups of a row,
+//                                                             one partial slot per K tile)
+// A wave covers one input block (all paths reading it with one mul2) and one
+// 16-wide K tile, so its gx entries are complete when it stores them.  The
+// 16x16 shape keeps the per-lane state small (4 dZ values per component).
+int ktiles16(const UvwPath& q) { return (q.mul1 * q.mul2 + 15) / 16; }
+
+std::string emit_backward_xy(const UvwSpec& s, const std::vector<Unit>& units, int phases) {
   Code c;
   c.s << kPrelude;
-  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_xy(");
-  c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
-  c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ gy, int B) {");
-  c.line("  __shared__ __attribute__((aligned(16))) real gs[%d][%d][%d];", d.d3max, kRows, GW);
-  c.line("  __shared__ __attribute__((aligned(16))) real ws[%d][%d];", d.kt, GW);
-  c.line("  __shared__ real dz[%d][%d][%d];", d.d3max, kRows, d.kt + 1);
-  c.line("  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;");
-  c.line("  const int b0 = blockIdx.x * %d;", kRows);
-  c.line("  const int half = lane >> 5, col = lane & 31;");
-  // First touch of each gx / gy range stores, later paths accumulate.
-  bool all_accumulate = false;
-  const std::vector<char> modes = gx_modes(s, &all_accumulate);
-  size_t tile_index = 0;
-  std::set<std::pair<int, int>> y_done;
-  for (const OutBlock& blk : out_blocks(s)) {
-    // Stage the output seed tile: gs[k][b][w] = g[b0+b, oo + w*d3 + k].
-    c.line("  __syncthreads();");
-    c.line("  for (int idx = tid; idx < %d; idx += 256) {", kRows * blk.mul3 * blk.d3);
-    c.line("    const int b = idx / %d, rest = idx - b * %d;", blk.mul3 * blk.d3, blk.mul3 * blk.d3);
-    c.line("    const int wch = rest / %d, k = rest - wch * %d;", blk.d3, blk.d3);
-    c.line("    const int row = b0 + b;");
-    c.line("    gs[k][b][wch] = row < B ? g[(i64)row * %d + %d + rest] : 0.0f;", s.out, blk.out_off);
-    c.line("  }");
-    if (round_up(blk.mul3, 32) > blk.mul3) {
-      c.line("  for (int idx = tid; idx < %d; idx += 256) {", kRows * blk.d3 * (d.npad - blk.mul3));
-      c.line("    const int pad = idx %% %d, rest = idx / %d;", d.npad - blk.mul3, d.npad - blk.mul3);
-      c.line("    gs[rest / %d][rest %% %d][%d + pad] = 0.0f;", kRows, kRows, blk.mul3);
-      c.line("  }");
-    }
-    const int nsteps = round_up(blk.mul3, 8) / 2;  // MFMA K steps over w, split in two halves
-    for (int p : blk.paths) {
-      const UvwPath& q = s.paths[p];
-      const int K = q.mul1 * q.mul2;
-      for (int k0 = 0; k0 < K; k0 += d.kt) {
-        const int ntile = (std::min(d.kt, K - k0) + 31) / 32;
-        const int tiles = q.d3 * ntile;
-        c.line("  __syncthreads();");
-        // ws[kk][w] = W[k0 + kk, w] (w contiguous, zero padded).
-        c.line("  for (int idx = tid; idx < %d; idx += 256) {", d.kt * d.npad);
-        c.line("    const int kk = idx / %d, n = idx - kk * %d, kg = %d + kk;", d.npad, d.npad, k0);
-        c.line("    ws[kk][n] = (kg < %d && n < %d) ? wt[%d + (i64)kg * %d + n] : 0.0f;", K, q.mul3, q.w_off, q.mul3);
-        c.line("  }");
-        c.line("  __syncthreads();");
-        // dZ[b, k, kk] = sum_w gs[k][b][w] ws[kk][w]: M = b, N = kk, K = w.
-        for (int t = 0; t < tiles; ++t) {
-          const int owner = t % 4, k = t / ntile, n0 = (t % ntile) * 32;
-          c.line("  if (wave == %d) {", owner);
-          c.line("    floatx16 a_acc = (floatx16)(0.0f);");
-          c.line("    for (int s = 0; s < %d; s += 4) {", nsteps);
-          c.line("      const float4 av = *(const float4*)&gs[%d][col][half * %d + s];", k, nsteps);
-          c.line("      const float4 bv = *(const float4*)&ws[%d + col][half * %d + s];", n0, nsteps);
-          c.line("      a_acc = mfma32(av.x, bv.x, a_acc);");
-          c.line("      a_acc = mfma32(av.y, bv.y, a_acc);");
-          c.line("      a_acc = mfma32(av.z, bv.z, a_acc);");
-          c.line("      a_acc = mfma32(av.w, bv.w, a_acc);");
-          c.line("    }");
-          c.line("    for (int r = 0; r < 16; ++r) dz[%d][8 * (r >> 2) + 4 * half + (r & 3)][%d + col] = a_acc[r];", k,
-                 n0);
-          c.line("  }");
+  c.s << R"(
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+// D[i][j] += sum_{k<4} A[i][k] B[k][j]; lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; register r of lane l holds D[4(l/16) + r][l%16].
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+)";
+  for (int phase = 0; phase < phases; ++phase) {
+    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_xy_p%d(", phase);
+    c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
+    c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B) {");
+    c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
+    c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
+    c.line("  const int b0 = (blockIdx.x * 4 + wave) * 16;");
+    c.line("  if (b0 >= B) return;");
+    c.line("  const bool rok = b0 + c16 < B;");
+    c.line("  const int brow = rok ? b0 + c16 : B - 1;");
+    c.line("  int unit = blockIdx.y;");
+    for (const Unit& un : units) {
+      if (un.phase != phase) continue;
+      const UvwPath& head = s.paths[un.paths[0]];
+      const int m2 = head.mul2, d1 = head.d1, Ktot = head.mul1 * head.mul2;
+      const int kts = ktiles16(head);
+      const int nq = 4 / m2;
+      std::map<int, std::string> cols;
+      for (int p : un.paths) {
+        const UvwPath& q = s.paths[p];
+        for (int v = 0; v < m2; ++v)
+          for (int j : term_js(q)) cols[q.y_off + v * q.d2 + j] = "gc" + std::to_string(q.y_off + v * q.d2 + j);
+      }
+      c.line("  if (unit < %d) {", kts);
+      c.line("    const int kt = unit;");
+      c.line("    const int ka = kt * 16 + c16;");  // A operand row (K index) of this lane
+      c.line("    const bool kaok = ka < %d;", Ktot);
+      c.line("    const int kb = kt * 16 + 4 * grp;");  // first of this lane's four D rows
+      for (int qd = 0; qd < nq; ++qd)
+        for (int i = 0; i < d1; ++i) c.line("    real gxa%d_%d = 0;", qd, i);
+      for (const auto& kv : cols) c.line("    real %s = 0;", kv.second.c_str());
+      // x of this lane's batch row at its four K indices.
+      c.line("    const real* xr = x + (i64)brow * %d + %d;", s.in1, head.x_off);
+      std::set<int> unit_is;
+      for (int p : un.paths)
+        for (int i : term_is(s.paths[p])) unit_is.insert(i);
+      for (int r = 0; r < 4; ++r) {
+        c.line("    const int u%d = (kb + %d < %d ? kb + %d : %d) / %d;", r, r, Ktot, r, Ktot - 1, m2);
+        for (int i : unit_is) c.line("    const real x%d_%d = xr[u%d * %d + %d];", r, i, r, d1, i);
+      }
+      for (int p : un.paths) {
+        const UvwPath& q = s.paths[p];
+        const int d3 = q.d3, mul3 = q.mul3;
+        const int steps = (mul3 + 3) / 4;
+        const std::set<int> js = term_js(q);
+        c.line("    {");
+        // A operand W_p[ka, 4s + grp] for every step, shared by all components.
+        c.line("      const real* wr = wt + %d + (i64)(kaok ? ka : %d) * %d;", q.w_off, Ktot - 1, mul3);
+        for (int st = 0; st < steps; ++st) {
+          const int w = 4 * st;
+          if (w + 3 < mul3)
+            c.line("      const real a%d = kaok ? wr[%d + grp] : 0.0f;", st, w);
+          else
+            c.line("      const real a%d = (kaok && %d + grp < %d) ? wr[%d + grp < %d ? %d + grp : %d] : 0.0f;", st, w,
+                   mul3, w, mul3, w, mul3 - 1);
         }
-        c.line("  __syncthreads();");
-        // gx[b, u, i] += sum_{v, j, k} c y_vj dZ[b, k, (u, v)]; gy[b, v, j] += sum_{u, i, k} c x_ui dZ[...].
-        // Wave w takes rows w, w+4, ...; lane = u (looping when mul1 > 64).
-        const int ku = std::min(d.kt, K - k0);
-        std::set<int> is, js;
-        for (const auto& t : q.terms) {
-          is.insert(t.i);
-          js.insert(t.j);
-        }
-        const bool x_first = modes[tile_index++] == 'S';
-        c.line("  for (int b = wave; b < %d; b += 4) {", kRows);
-        c.line("    const int row = b0 + b;");
-        c.line("    if (row >= B) break;");
-        // y values of this row (uniform).
-        c.line("    const real* yq = y + (i64)row * %d + %d;", s.in2, q.y_off);
-        for (int v = 0; v < q.mul2; ++v)
-          for (int j : js) c.line("    real gy%d_%d = 0;", v, j);
-        c.line("    for (int uu = lane; uu < %d; uu += 64) {", (ku + q.mul2 - 1) / q.mul2);
-        c.line("      const int u = %d + uu;", k0 / q.mul2);
-        c.line("      const real* xq = x + (i64)row * %d + %d + u * %d;", s.in1, q.x_off, q.d1);
-        for (int i : is) c.line("      const real px%d = xq[%d];", i, i);
-        for (int i : is) c.line("      real ax%d = 0;", i);
-        for (int v = 0; v < q.mul2; ++v) {
+        c.line("      const real* gr = g + (i64)brow * %d + %d;", s.out, q.out_off);
+        c.line("      const real* yr = y + (i64)brow * %d + %d;", s.in2, q.y_off);
+        for (int v = 0; v < m2; ++v)
+          for (int j : js) c.line("      const real y%d_%d = yr[%d];", v, j, v * q.d2 + j);
+        for (int v = 0; v < m2; ++v)
+          for (int j : js) c.line("      real gp%d_%d = 0;", v, j);
+        for (int k = 0; k < d3; ++k) {
+          bool any = false;
+          for (const auto& t : q.terms) any = any || t.k == k;
+          if (!any) continue;
           c.line("      {");
-          c.line("        const int kk = uu * %d + %d;", q.mul2, v);
-          for (int k = 0; k < q.d3; ++k) c.line("        const real dz%d = dz[%d][b][kk];", k, k);
-          for (const auto& t : q.terms) {
-            c.line("        ax%d = FMA(%s, yq[%d] * dz%d, ax%d);", t.i, flit(t.c).c_str(), v * q.d2 + t.j, t.k, t.i);
-            c.line("        gy%d_%d = FMA(%s, px%d * dz%d, gy%d_%d);", v, t.j, flit(t.c).c_str(), t.i, t.k, v, t.j);
+          c.line("        floatx4 dz = (floatx4)(0.0f);");
+          for (int st = 0; st < steps; ++st) {
+            const int w = 4 * st;
+            if (w + 3 < mul3)
+              c.line("        dz = mfma16(a%d, gr[(%d + grp) * %d + %d], dz);", st, w, d3, k);
+            else
+              c.line("        dz = mfma16(a%d, gr[(%d + grp < %d ? %d + grp : %d) * %d + %d], dz);", st, w, mul3, w,
+                     mul3 - 1, d3, k);
+          }
+          for (int r = 0; r < 4; ++r) {
+            const int v = r % m2, qd = r / m2;
+            for (const auto& t : q.terms) {
+              if (t.k != k) continue;
+              c.line("        gxa%d_%d = FMA(%s * y%d_%d, dz[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, r,
+                     qd, t.i);
+              c.line("        gp%d_%d = FMA(%s * x%d_%d, dz[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, r, v,
+                     t.j);
+            }
           }
           c.line("      }");
         }
-        c.line("      real* gq = gx + (i64)row * %d + %d + u * %d;", s.in1, q.x_off, q.d1);
-        for (int i = 0; i < q.d1; ++i) {
-          const std::string value = is.count(i) ? "ax" + std::to_string(i) : std::string("0.0f");
-          if (x_first)
-            c.line("      gq[%d] = %s;", i, value.c_str());
-          else if (is.count(i))
-            c.line("      gq[%d] += %s;", i, value.c_str());
-        }
-        c.line("    }");
-        // Sum the gy partials over the 64 lanes and let lane 0 write them.
-        for (int v = 0; v < q.mul2; ++v)
+        // Sum over the four lane groups that share a batch row.
+        for (int v = 0; v < m2; ++v)
           for (int j : js) {
-            c.line("    for (int m = 32; m >= 1; m >>= 1) gy%d_%d += __shfl_xor(gy%d_%d, m, 64);", v, j, v, j);
-          }
-        const bool y_first = y_done.insert({q.y_off, 0}).second && k0 == 0;
-        c.line("    if (lane == 0) {");
-        c.line("      real* gq = gy + (i64)row * %d + %d;", s.in2, q.y_off);
-        for (int v = 0; v < q.mul2; ++v)
-          for (int j = 0; j < q.d2; ++j) {
-            const std::string value = js.count(j) ? "gy" + std::to_string(v) + "_" + std::to_string(j) : "0.0f";
-            if (y_first)
-              c.line("      gq[%d] = %s;", v * q.d2 + j, value.c_str());
-            else if (js.count(j))
-              c.line("      gq[%d] += %s;", v * q.d2 + j, value.c_str());
+            c.line("      gp%d_%d += __shfl_xor(gp%d_%d, 16, 64);", v, j, v, j);
+            c.line("      gp%d_%d += __shfl_xor(gp%d_%d, 32, 64);", v, j, v, j);
+            c.line("      %s += gp%d_%d;", cols[q.y_off + v * q.d2 + j].c_str(), v, j);
           }
         c.line("    }");
-        c.line("  }");
       }
+      c.line("    if (rok) {");
+      c.line("      real* gq = gx + (i64)brow * %d + %d;", s.in1, head.x_off);
+      for (int qd = 0; qd < nq; ++qd) {
+        const int r = qd * m2;
+        c.line("      if (kb + %d < %d) {", r, Ktot);
+        c.line("        const int ur = (kb + %d) / %d;", r, m2);
+        for (int i = 0; i < d1; ++i)
+          c.line("        gq[ur * %d + %d] %s gxa%d_%d;", d1, i, un.accumulate ? "+=" : "=", qd, i);
+        c.line("      }");
+      }
+      c.line("      if (grp == 0) {");
+      c.line("        real* pr = part + ((i64)(%d + kt) * B + brow) * %d;", un.slot_base, s.in2);
+      for (const auto& kv : cols) c.line("        pr[%d] = %s;", kv.first, kv.second.c_str());
+      c.line("      }");
+      c.line("    }");
+      c.line("    return;");
+      c.line("  }");
+      c.line("  unit -= %d;", kts);
     }
+    c.line("}");
+  }
+  // gy[b, col] = sum of the partial slots that hold column col.
+  std::vector<std::vector<int>> writers(s.in2);
+  for (const Unit& un : units) {
+    const UvwPath& head = s.paths[un.paths[0]];
+    std::set<int> cols;
+    for (int p : un.paths) {
+      const UvwPath& q = s.paths[p];
+      for (int v = 0; v < q.mul2; ++v)
+        for (int j : term_js(q)) cols.insert(q.y_off + v * q.d2 + j);
+    }
+    for (int col : cols)
+      for (int kt = 0; kt < ktiles16(head); ++kt) writers[col].push_back(un.slot_base + kt);
+  }
+  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_gy(");
+  c.line("    const real* __restrict__ part, real* __restrict__ gy, int B) {");
+  c.line("  const int b = blockIdx.x * 256 + threadIdx.x;");
+  c.line("  if (b >= B) return;");
+  for (int col = 0; col < s.in2; ++col) {
+    std::string sum;
+    for (int slot : writers[col]) {
+      char term[96];
+      std::snprintf(term, sizeof(term), "part[((i64)%d * B + b) * %d + %d]", slot, s.in2, col);
+      sum += (sum.empty() ? "" : " + ") + std::string(term);
+    }
+    c.line("  gy[(i64)b * %d + %d] = %s;", s.in2, col, sum.empty() ? "0.0f" : sum.c_str());
   }
   c.line("}");
   return c.s.str();
 }
 
 // ---------------------------------------------------------------- backward: weights
+// dW_p[K, w] = sum_{b,k} Z_p[b, k, K] g[b, oo + w*d3 + k]: A = Z_p (rows K,
+// produced in-lane for K = 32 mt + l%32 from batch row 2s + l/32), B = the
+// seed rows (columns w), contraction over (b, k) two batch rows per
+// instruction and one instruction per k.  Each wave owns kChunkRows rows of
+// one path and writes one partial of dW_p; a second kernel sums the partials.
 std::string emit_backward_w(const UvwSpec& s) {
-  const Dims d = dims(s);
   Code c;
   c.s << kPrelude;
-  // One kernel per path (launch grid.y = path); each workgroup accumulates
-  // dW_p over kChunkTiles row tiles and writes one partial.
+  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w(");
+  c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ g,");
+  c.line("    real* __restrict__ part, int B) {");
+  emit_head(c);
+  c.line("  const int chunk = blockIdx.x * 4 + wave;");
+  c.line("  const int r0 = chunk * %d;", kChunkRows);
+  c.line("  if (r0 >= B) return;");
+  c.line("  const int path = blockIdx.y;");
   for (int p = 0; p < (int)s.paths.size(); ++p) {
     const UvwPath& q = s.paths[p];
-    const int K = q.mul1 * q.mul2;
-    const int Q = kRows * q.d3;          // MFMA K extent per row tile: (b, k) pairs
-    const int QP = round_up(Q, 8);       // padded to two halves of 4-steps
-    const int mt = round_up(K, 32) / 32, nt = round_up(q.mul3, 32) / 32;
-    const int tiles = mt * nt;
-    const int per_wave = (tiles + 3) / 4;
-    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w%d(", p);
-    c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ g,");
-    c.line("    real* __restrict__ part, int B) {");
-    c.line("  __shared__ __attribute__((aligned(16))) real zs[%d][%d];", mt * 32, QP + 4);
-    c.line("  __shared__ __attribute__((aligned(16))) real gs[%d][%d];", nt * 32, QP + 4);
-    c.line("  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;");
-    c.line("  const int half = lane >> 5, col = lane & 31;");
-    c.line("  floatx16 acc[%d];", per_wave);
-    c.line("  for (int t = 0; t < %d; ++t) acc[t] = (floatx16)(0.0f);", per_wave);
-    c.line("  for (int tile = 0; tile < %d; ++tile) {", kChunkTiles);
-    c.line("    const int b0 = (blockIdx.x * %d + tile) * %d;", kChunkTiles, kRows);
-    c.line("    if (b0 >= B) break;");
-    c.line("    __syncthreads();");
-    // zs[K][(b,k)] = Z_p[b, k, K]
-    c.line("    for (int idx = tid; idx < %d; idx += 256) {", kRows * mt * 32);
-    c.line("      const int kg = idx %% %d, b = idx / %d;", mt * 32, mt * 32);
-    c.line("      const int row = b0 + b;");
-    c.line("      if (kg < %d && row < B) {", K);
-    emit_producer(c, s, q, "row", "kg", "        ");
-    for (int k = 0; k < q.d3; ++k) c.line("        zs[kg][b * %d + %d] = z%d;", q.d3, k, k);
-    c.line("      } else {");
-    for (int k = 0; k < q.d3; ++k) c.line("        zs[kg][b * %d + %d] = 0.0f;", q.d3, k);
-    c.line("      }");
-    c.line("    }");
-    // gs[w][(b,k)] = g[b0+b, oo + w*d3 + k]
-    c.line("    for (int idx = tid; idx < %d; idx += 256) {", kRows * nt * 32 * q.d3);
-    c.line("      const int b = idx / %d, rest = idx - b * %d;", nt * 32 * q.d3, nt * 32 * q.d3);
-    c.line("      const int wch = rest / %d, k = rest - wch * %d;", q.d3, q.d3);
-    c.line("      const int row = b0 + b;");
-    c.line("      gs[wch][b * %d + k] = (row < B && wch < %d) ? g[(i64)row * %d + %d + rest] : 0.0f;", q.d3, q.mul3,
-           s.out, q.out_off);
-    c.line("    }");
-    if (QP > Q) {
-      c.line("    for (int idx = tid; idx < %d; idx += 256) {", (QP - Q) * (mt * 32 + nt * 32));
-      c.line("      const int r = idx / %d, pad = idx - r * %d;", QP - Q, QP - Q);
-      c.line("      if (r < %d) zs[r][%d + pad] = 0.0f; else gs[r - %d][%d + pad] = 0.0f;", mt * 32, Q, mt * 32, Q);
-      c.line("    }");
+    const int K = q.mul1 * q.mul2, mt = ktiles(q), nt = (q.mul3 + 31) / 32, d3 = q.d3;
+    const std::set<int> is = term_is(q), js = term_js(q);
+    c.line("  if (path == %d) {", p);
+    for (int m = 0; m < mt; ++m)
+      for (int n = 0; n < nt; ++n) c.line("    floatx16 acc%d_%d = (floatx16)(0.0f);", m, n);
+    for (int m = 0; m < mt; ++m) {
+      c.line("    const int k%d = %d + col;", m, m * 32);
+      c.line("    const int u%d = (k%d < %d ? k%d : %d) / %d, v%d = (k%d < %d ? k%d : %d) %% %d;", m, m, K, m, K - 1,
+             q.mul2, m, m, K, m, K - 1, q.mul2);
+      c.line("    const bool kok%d = k%d < %d;", m, m, K);
     }
-    c.line("    __syncthreads();");
-    for (int t = 0; t < tiles; ++t) {
-      const int owner = t % 4, slot = t / 4, m0 = (t / nt) * 32, n0 = (t % nt) * 32;
-      c.line("    if (wave == %d) {", owner);
-      c.line("      floatx16 a_acc = acc[%d];", slot);
-      c.line("      for (int s = 0; s < %d; s += 4) {", QP / 2);
-      c.line("        const float4 av = *(const float4*)&zs[%d + col][half * %d + s];", m0, QP / 2);
-      c.line("        const float4 bv = *(const float4*)&gs[%d + col][half * %d + s];", n0, QP / 2);
-      c.line("        a_acc = mfma32(av.x, bv.x, a_acc);");
-      c.line("        a_acc = mfma32(av.y, bv.y, a_acc);");
-      c.line("        a_acc = mfma32(av.z, bv.z, a_acc);");
-      c.line("        a_acc = mfma32(av.w, bv.w, a_acc);");
-      c.line("      }");
-      c.line("      acc[%d] = a_acc;", slot);
-      c.line("    }");
+    for (int n = 0; n < nt; ++n) {
+      c.line("    const int w%d = %d + col;", n, n * 32);
+      c.line("    const bool wok%d = w%d < %d;", n, n, q.mul3);
     }
+    c.line("    #pragma unroll 2");
+    c.line("    for (int s = 0; s < %d; ++s) {", kChunkRows / 2);
+    c.line("      const int row = r0 + 2 * s + hk;");
+    c.line("      const bool rok = row < B;");
+    c.line("      const int rc = rok ? row : B - 1;");
+    c.line("      const real* xr = x + (i64)rc * %d + %d;", s.in1, q.x_off);
+    c.line("      const real* yr = y + (i64)rc * %d + %d;", s.in2, q.y_off);
+    c.line("      const real* gr = g + (i64)rc * %d + %d;", s.out, q.out_off);
+    for (int m = 0; m < mt; ++m) {
+      c.line("      const bool zok%d = rok && kok%d;", m, m);
+      for (int i : is) c.line("      const real x%d_%d = xr[u%d * %d + %d];", m, i, m, q.d1, i);
+      for (int j : js) c.line("      const real y%d_%d = yr[v%d * %d + %d];", m, j, m, q.d2, j);
+      for (int k = 0; k < d3; ++k) c.line("      real z%d_%d = 0;", m, k);
+      for (const auto& t : q.terms)
+        c.line("      z%d_%d = FMA(%s, x%d_%d * y%d_%d, z%d_%d);", m, t.k, flit(t.c).c_str(), m, t.i, m, t.j, m, t.k);
+      for (int k = 0; k < d3; ++k) c.line("      z%d_%d = zok%d ? z%d_%d : 0.0f;", m, k, m, m, k);
+    }
+    for (int n = 0; n < nt; ++n)
+      for (int k = 0; k < d3; ++k)
+        c.line("      const real g%d_%d = (rok && wok%d) ? gr[(wok%d ? w%d : 0) * %d + %d] : 0.0f;", n, k, n, n, n, d3,
+               k);
+    for (int k = 0; k < d3; ++k)
+      for (int m = 0; m < mt; ++m)
+        for (int n = 0; n < nt; ++n) c.line("      acc%d_%d = mfma32(z%d_%d, g%d_%d, acc%d_%d);", m, n, m, k, n, k, m, n);
+    c.line("    }");
+    // Register r: K = 32 m + 8(r/4) + 4hk + r%4, w = 32 n + col.
+    c.line("    real* pr = part + (i64)chunk * %d + %d;", s.wnum, q.w_off);
+    for (int m = 0; m < mt; ++m)
+      for (int n = 0; n < nt; ++n) {
+        c.line("    if (wok%d) {", n);
+        c.line("      #pragma unroll");
+        c.line("      for (int r = 0; r < 16; ++r) {");
+        c.line("        const int kr = %d + 8 * (r >> 2) + 4 * hk + (r & 3);", m * 32);
+        c.line("        if (kr < %d) pr[(i64)kr * %d + w%d] = acc%d_%d[r];", K, q.mul3, n, m, n);
+        c.line("      }");
+        c.line("    }");
+      }
+    c.line("    return;");
     c.line("  }");
-    // part[chunk][wo + K*mul3 + w]
-    for (int t = 0; t < tiles; ++t) {
-      const int owner = t % 4, slot = t / 4, m0 = (t / nt) * 32, n0 = (t % nt) * 32;
-      c.line("  if (wave == %d && %d + col < %d) {", owner, n0, q.mul3);
-      c.line("    for (int r = 0; r < 16; ++r) {");
-      c.line("      const int kg = %d + 8 * (r >> 2) + 4 * half + (r & 3);", m0);
-      c.line("      if (kg < %d) part[(i64)blockIdx.x * %d + %d + kg * %d + %d + col] = acc[%d][r];", K, s.wnum,
-             q.w_off, q.mul3, n0, slot);
-      c.line("    }");
-      c.line("  }");
-    }
-    c.line("}");
   }
+  c.line("}");
+  // gw[i] = sum over chunks of part[chunk][i], for the covered entries.
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w_reduce(");
   c.line("    const real* __restrict__ part, real* __restrict__ gw, int chunks) {");
   c.line("  const int i = blockIdx.x * 256 + threadIdx.x;");
   c.line("  if (i >= %d) return;", s.wnum);
+  std::string covered;
+  for (const auto& q : s.paths) {
+    char term[96];
+    std::snprintf(term, sizeof(term), "(i >= %d && i < %d)", q.w_off, q.w_off + q.mul1 * q.mul2 * q.mul3);
+    covered += (covered.empty() ? "" : " || ") + std::string(term);
+  }
+  c.line("  if (!(%s)) return;", covered.c_str());
   c.line("  real acc = 0;");
   c.line("  for (int n = 0; n < chunks; ++n) acc += part[(i64)n * %d + i];", s.wnum);
   c.line("  gw[i] = acc;");
@@ -534,12 +575,16 @@ std::string emit_backward_w(const UvwSpec& s) {
 struct UvwPlan {
   UvwSpec spec;
   ModuleCache kernels;
+  std::vector<Unit> fwd_units, bwd_units;
+  int fwd_phases = 0, bwd_phases = 0;
+  std::vector<int> fwd_phase_tiles, bwd_phase_tiles;  // grid.y per phase
+  int gy_slots = 0;
   bool out_needs_zero = false, gx_needs_zero = false, gy_needs_zero = false, gw_needs_zero = false;
 };
 
 std::string source_for(const UvwPlan& plan, const std::string& variant) {
-  if (variant == "fwd") return emit_forward(plan.spec);
-  if (variant == "bxy") return emit_backward_xy(plan.spec);
+  if (variant == "fwd") return emit_forward(plan.spec, plan.fwd_units, plan.fwd_phases);
+  if (variant == "bxy") return emit_backward_xy(plan.spec, plan.bwd_units, plan.bwd_phases);
   return emit_backward_w(plan.spec);
 }
 
@@ -569,9 +614,17 @@ hipModule_t module_for(UvwPlan& plan, const std::string& variant) {
   return plan.kernels.module_for(variant, [&] { return source_for(plan, variant); });
 }
 
-int64_t chunks_for(int64_t rows) {
-  const int64_t per = (int64_t)kRows * kChunkTiles;
-  return (rows + per - 1) / per;
+int64_t chunks_for(int64_t rows) { return (rows + kChunkRows - 1) / kChunkRows; }
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+size_t gw_part_bytes(const UvwPlan& p, int64_t rows) {
+  return align256((size_t)chunks_for(rows) * (size_t)p.spec.wnum * sizeof(float));
+}
+size_t gy_part_bytes(const UvwPlan& p, int64_t rows) {
+  return align256((size_t)p.gy_slots * (size_t)rows * (size_t)p.spec.in2 * sizeof(float));
+}
+unsigned row_blocks(int64_t rows, int rows_per_wave) {  // 4 waves per workgroup
+  return (unsigned)((rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave));
 }
 
 }  // namespace
@@ -586,18 +639,35 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.spec = parse(spec);
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
     p.kernels.tag = "uvw";
-    std::vector<std::pair<long, long>> outs, xs, ys, ws;
+    std::vector<std::pair<long, long>> xs, ws;
     for (const auto& q : p.spec.paths) {
-      outs.push_back({q.out_off, q.out_off + (long)q.mul3 * q.d3});
       xs.push_back({q.x_off, q.x_off + (long)q.mul1 * q.d1});
-      ys.push_back({q.y_off, q.y_off + (long)q.mul2 * q.d2});
       ws.push_back({q.w_off, q.w_off + (long)q.mul1 * q.mul2 * q.mul3});
     }
-    p.out_needs_zero = !covers(outs, p.spec.out);
-    bool all_accumulate = false;
-    gx_modes(p.spec, &all_accumulate);
-    p.gx_needs_zero = !covers(xs, p.spec.in1) || all_accumulate;
-    p.gy_needs_zero = !covers(ys, p.spec.in2);
+    p.fwd_units = forward_units(p.spec);
+    bool out_collision = false, gx_collision = false;
+    p.fwd_phases = assign_phases(p.fwd_units, &out_collision);
+    p.fwd_phase_tiles.assign(p.fwd_phases, 0);
+    std::vector<std::pair<long, long>> outs;
+    for (const Unit& u : p.fwd_units) {
+      p.fwd_phase_tiles[u.phase] += (p.spec.paths[u.paths[0]].mul3 + 31) / 32;
+      outs.push_back({u.lo, u.hi});
+    }
+    p.bwd_units = backward_units(p.spec);
+    p.bwd_phases = assign_phases(p.bwd_units, &gx_collision);
+    p.bwd_phase_tiles.assign(p.bwd_phases, 0);
+    for (Unit& u : p.bwd_units) {
+      u.slot_base = p.gy_slots;
+      p.gy_slots += ktiles16(p.spec.paths[u.paths[0]]);
+      p.bwd_phase_tiles[u.phase] += ktiles16(p.spec.paths[u.paths[0]]);
+    }
+    for (int t : p.fwd_phase_tiles)
+      if (t > 65535) fail("uvw: too many output tiles for one launch");
+    for (int t : p.bwd_phase_tiles)
+      if (t > 65535) fail("uvw: too many K tiles for one launch");
+    p.out_needs_zero = out_collision || !covers(outs, p.spec.out);
+    p.gx_needs_zero = gx_collision || !covers(xs, p.spec.in1);
+    p.gy_needs_zero = false;  // the gy reduction writes every column
     p.gw_needs_zero = !covers(ws, p.spec.wnum);
     *out = holder.release();
   });
@@ -635,9 +705,11 @@ int luna_uvw_fwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
     UvwPlan& plan = const_cast<LunaUvwPlan*>(cplan)->plan;
     hipModule_t module = module_for(plan, "fwd");
     int B = (int)rows;
-    void* args[] = {&x, &y, &weight, &out, &B};
-    launch("uvw_fwd", function_for(module, "luna_uvw_fwd"), dim3((unsigned)((rows + kRows - 1) / kRows)), dim3(256),
-           (hipStream_t)stream, args);
+    for (int phase = 0; phase < plan.fwd_phases; ++phase) {
+      void* args[] = {&x, &y, &weight, &out, &B};
+      launch("uvw_fwd", function_for(module, "luna_uvw_fwd_p" + std::to_string(phase)),
+             dim3(row_blocks(rows, 32), (unsigned)plan.fwd_phase_tiles[phase]), dim3(256), (hipStream_t)stream, args);
+    }
   });
 }
 
@@ -645,7 +717,7 @@ int luna_uvw_bwd_workspace(const LunaUvwPlan* plan, int64_t rows, size_t* bytes)
   return guard_call([&] {
     if (!plan || !bytes) fail("luna_uvw_bwd_workspace: null argument");
     if (rows < 0) fail("negative row count");
-    *bytes = (size_t)chunks_for(rows) * (size_t)plan->plan.spec.wnum * sizeof(float);
+    *bytes = gw_part_bytes(plan->plan, rows) + gy_part_bytes(plan->plan, rows);
   });
 }
 
@@ -659,27 +731,34 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
     UvwPlan& plan = const_cast<LunaUvwPlan*>(cplan)->plan;
     hipStream_t s = (hipStream_t)stream;
     int B = (int)rows;
+    const size_t need = gw_part_bytes(plan, rows) + gy_part_bytes(plan, rows);
+    if (rows > 0 && (gx || gy || gw) && (!workspace || workspace_bytes < need))
+      fail("luna_uvw_bwd: workspace too small");
+    char* ws = (char*)workspace;
+    void* gw_part = ws;
+    void* gy_part = ws + gw_part_bytes(plan, rows);
     if ((gx || gy) && rows > 0) {
       if (!gx || !gy) fail("luna_uvw_bwd: gx and gy are produced together");
       hipModule_t module = module_for(plan, "bxy");
-      void* args[] = {&x, &y, &weight, &g, &gx, &gy, &B};
-      launch("uvw_bwd_xy", function_for(module, "luna_uvw_bwd_xy"), dim3((unsigned)((rows + kRows - 1) / kRows)),
-             dim3(256), s, args);
+      for (int phase = 0; phase < plan.bwd_phases; ++phase) {
+        void* args[] = {&x, &y, &weight, &g, &gx, &gy_part, &B};
+        launch("uvw_bwd_xy", function_for(module, "luna_uvw_bwd_xy_p" + std::to_string(phase)),
+               dim3(row_blocks(rows, 16), (unsigned)plan.bwd_phase_tiles[phase]), dim3(256), s, args);
+      }
+      void* args[] = {&gy_part, &gy, &B};
+      launch("uvw_bwd_gy", function_for(module, "luna_uvw_bwd_gy"), dim3((unsigned)((rows + 255) / 256)), dim3(256),
+             s, args);
     }
     if (gw) {
-      const int64_t chunks = chunks_for(rows);
-      const size_t need = (size_t)chunks * (size_t)plan.spec.wnum * sizeof(float);
-      if (rows > 0 && (!workspace || workspace_bytes < need)) fail("luna_uvw_bwd: workspace too small");
       hipModule_t module = module_for(plan, "bw");
+      const int64_t chunks = chunks_for(rows);
       if (rows > 0) {
-        for (int p = 0; p < (int)plan.spec.paths.size(); ++p) {
-          void* args[] = {&x, &y, &g, &workspace, &B};
-          launch("uvw_bwd_w", function_for(module, "luna_uvw_bwd_w" + std::to_string(p)), dim3((unsigned)chunks),
-                 dim3(256), s, args);
-        }
+        void* args[] = {&x, &y, &g, &gw_part, &B};
+        launch("uvw_bwd_w", function_for(module, "luna_uvw_bwd_w"),
+               dim3((unsigned)((chunks + 3) / 4), (unsigned)plan.spec.paths.size()), dim3(256), s, args);
       }
       int n = (int)chunks;
-      void* args[] = {&workspace, &gw, &n};
+      void* args[] = {&gw_part, &gw, &n};
       launch("uvw_bwd_w_reduce", function_for(module, "luna_uvw_bwd_w_reduce"),
              dim3((unsigned)((plan.spec.wnum + 255) / 256)), dim3(256), s, args);
     }

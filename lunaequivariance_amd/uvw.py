@@ -148,6 +148,7 @@ def run_backward(op, x, y, w, g, needs=(True, True, True)):
     size = ctypes.c_size_t(0)
     if needs[2]:
         gw = (torch.zeros if plan.gw_zero else torch.empty)(w.shape, device=x.device, dtype=x.dtype)
+    if want_xy or needs[2]:
         _native.check(_native.lib().luna_uvw_bwd_workspace(plan.handle, rows, ctypes.byref(size)),
                       "luna_uvw_bwd_workspace")
         workspace = torch.empty(max(size.value, 4), device=x.device, dtype=torch.uint8)
