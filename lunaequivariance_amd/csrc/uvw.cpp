@@ -41,6 +41,7 @@ struct UvwSpec {
 };
 
 constexpr int kChunkRows = 256;  // batch rows per wave (and per partial) of the weight gradient
+constexpr int kReduceGroups = 16;  // parallel groups of partials in the weight-gradient reduction
 
 int read_int(std::istringstream& in, const char* what) {
   long long value;
@@ -196,6 +197,29 @@ std::vector<Unit> backward_units(const UvwSpec& s) {
 
 int ktiles(const UvwPath& q) { return (q.mul1 * q.mul2 + 31) / 32; }
 
+// 16-byte loads along a lane's own row where the layout allows
+// (LUNAEQ_AMD_UVW_VEC=0 turns them off, for comparison).
+bool vector_loads() {
+  const char* e = std::getenv("LUNAEQ_AMD_UVW_VEC");
+  return !e || std::atoi(e) != 0;
+}
+
+constexpr int kStageU = 16;  // channels u per LDS chunk of the forward's x staging
+
+// Forward paths whose x block is staged through LDS (16-byte aligned rows,
+// whole chunks of channels, one y copy).
+bool staged_path(const UvwSpec& s, const UvwPath& q) {
+  return vector_loads() && q.mul2 == 1 && q.mul1 % kStageU == 0 && q.x_off % 4 == 0 && s.in1 % 4 == 0 &&
+         (kStageU * q.d1) % 4 == 0;
+}
+
+
+// Backward paths whose seed rows and weights are staged through LDS in
+// chunks of 16 output channels.
+bool staged_seeds(const UvwSpec& s, const UvwPath& q) {
+  return vector_loads() && q.mul3 % 16 == 0 && q.out_off % 4 == 0 && s.out % 4 == 0 && q.w_off % 4 == 0;
+}
+
 // Sorted distinct (i) and (j) indices of a path's terms.
 std::set<int> term_is(const UvwPath& q) {
   std::set<int> r;
@@ -240,6 +264,13 @@ std::string emit_forward(const UvwSpec& s, const std::vector<Unit>& units, int p
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    real* __restrict__ out, int B) {");
     emit_head(c);
+    int stage_d1 = 0;
+    for (const Unit& u : units)
+      if (u.phase == phase)
+        for (int p : u.paths)
+          if (staged_path(s, s.paths[p])) stage_d1 = std::max(stage_d1, s.paths[p].d1);
+    // Row pitch kStageU*d1 + 1: the 32 rows read at one offset fall in 32 banks.
+    if (stage_d1) c.line("  __shared__ real xs[4][32][%d];", kStageU * stage_d1 + 1);
     c.line("  const int b0 = (blockIdx.x * 4 + wave) * 32;");
     c.line("  if (b0 >= B) return;");
     c.line("  const int brow = b0 + col < B ? b0 + col : B - 1;");
@@ -263,11 +294,43 @@ std::string emit_forward(const UvwSpec& s, const std::vector<Unit>& units, int p
         c.line("      const real* wr = wt + %d + (wok ? w0 + col : 0);", q.w_off);
         if (q.mul2 == 1)
           for (int j : js) c.line("      const real y%d = yr[%d];", j, j);
+        const int half = (K + 1) / 2;
+        if (staged_path(s, q)) {
+          // The x block of the wave's 32 rows goes through LDS in chunks of
+          // kStageU channels, read from HBM with consecutive lanes on
+          // consecutive addresses (a lane-per-row gather costs one cache
+          // line per lane in the address unit); lanes then read their own row.
+          const int chd = kStageU * q.d1;
+          c.line("      for (int c0 = 0; c0 < %d; c0 += %d) {", q.mul1, kStageU);
+          c.line("        const float4* xg = (const float4*)(x + %d + c0 * %d);", q.x_off, q.d1);
+          c.line("        #pragma unroll 2");
+          c.line("        for (int it = 0; it < %d; ++it) {", 32 * chd / 4 / 64);
+          c.line("          const int idx = it * 64 + lane, r = idx / %d, e = idx - r * %d;", chd / 4, chd / 4);
+          c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
+          c.line("          const float4 v = xg[(i64)rr * %d + e];", s.in1 / 4);
+          c.line("          real* dst = &xs[wave][r][e * 4];");
+          c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
+          c.line("        }");
+          c.line("        const real* xl = &xs[wave][col][0];");
+          c.line("        #pragma unroll 4");
+          c.line("        for (int s = 0; s < %d; ++s) {", kStageU / 2);
+          c.line("          const int ul = 2 * s + hk, kk = c0 + ul;");
+          for (int i : is) c.line("          const real x%d = xl[ul * %d + %d];", i, q.d1, i);
+          c.line("          const real a = wok ? wr[(i64)kk * %d] : 0.0f;", mul3);
+          for (int k = 0; k < d3; ++k) c.line("          real z%d = 0;", k);
+          for (const auto& t : q.terms)
+            c.line("          z%d = FMA(%s, x%d * y%d, z%d);", t.k, flit(t.c).c_str(), t.i, t.j, t.k);
+          for (int k = 0; k < d3; ++k) c.line("          acc%d = mfma32(a, z%d, acc%d);", k, k, k);
+          c.line("        }");
+          c.line("      }");
+          c.line("    }");
+          continue;
+        }
         c.line("      #pragma unroll 4");
-        c.line("      for (int s = 0; s < %d; ++s) {", (K + 1) / 2);
+        c.line("      for (int s = 0; s < %d; ++s) {", half);
         // An odd K leaves the last upper-half lane without a pair: its A is
-        // zero and its loads use the last valid pair.
-        c.line("        const int kk = 2 * s + hk;");
+        // zero and its loads use the last valid entry.
+        c.line("        const int kk = s + hk * %d;", half);
         c.line("        const bool kok = kk < %d;", K);
         c.line("        const int kc = kok ? kk : %d;", K - 1);
         c.line("        const int u = kc / %d, v = kc %% %d;", q.mul2, q.mul2);
@@ -335,6 +398,15 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B) {");
     c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
+    int stage_d3 = 0;
+    for (const Unit& u : units)
+      if (u.phase == phase)
+        for (int p : u.paths)
+          if (staged_seeds(s, s.paths[p])) stage_d3 = std::max(stage_d3, s.paths[p].d3);
+    if (stage_d3) {
+      c.line("  __shared__ real gs[4][16][%d];", 16 * stage_d3 + 1);
+      c.line("  __shared__ real wsh[4][16][17];");
+    }
     c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
     c.line("  const int b0 = (blockIdx.x * 4 + wave) * 16;");
     c.line("  if (b0 >= B) return;");
@@ -366,57 +438,91 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       std::set<int> unit_is;
       for (int p : un.paths)
         for (int i : term_is(s.paths[p])) unit_is.insert(i);
-      for (int r = 0; r < 4; ++r) {
-        c.line("    const int u%d = (kb + %d < %d ? kb + %d : %d) / %d;", r, r, Ktot, r, Ktot - 1, m2);
-        for (int i : unit_is) c.line("    const real x%d_%d = xr[u%d * %d + %d];", r, i, r, d1, i);
+      if (vector_loads() && m2 == 1 && Ktot % 16 == 0 && head.x_off % 4 == 0 && s.in1 % 4 == 0) {
+        // The four K indices of the lane are four consecutive u: 4*d1 floats.
+        c.line("    const float4* xv = (const float4*)(xr + (i64)kb * %d);", d1);
+        for (int v4 = 0; v4 < d1; ++v4) c.line("    const float4 xq%d = xv[%d];", v4, v4);
+        for (int r = 0; r < 4; ++r)
+          for (int i : unit_is) {
+            const int e = r * d1 + i;
+            c.line("    const real x%d_%d = xq%d.%c;", r, i, e / 4, "xyzw"[e % 4]);
+          }
+      } else {
+        for (int r = 0; r < 4; ++r) {
+          c.line("    const int u%d = (kb + %d < %d ? kb + %d : %d) / %d;", r, r, Ktot, r, Ktot - 1, m2);
+          for (int i : unit_is) c.line("    const real x%d_%d = xr[u%d * %d + %d];", r, i, r, d1, i);
+        }
       }
       for (int p : un.paths) {
         const UvwPath& q = s.paths[p];
         const int d3 = q.d3, mul3 = q.mul3;
-        const int steps = (mul3 + 3) / 4;
+        const int quarter = (mul3 + 3) / 4;
         const std::set<int> js = term_js(q);
+        // Lane group grp contracts w in [grp*quarter, grp*quarter + quarter),
+        // so each lane's W and g entries are consecutive (16-byte loads of four
+        // steps when the layout allows it).
+        const bool vec = staged_seeds(s, q);
         c.line("    {");
-        // A operand W_p[ka, 4s + grp] for every step, shared by all components.
-        c.line("      const real* wr = wt + %d + (i64)(kaok ? ka : %d) * %d;", q.w_off, Ktot - 1, mul3);
-        for (int st = 0; st < steps; ++st) {
-          const int w = 4 * st;
-          if (w + 3 < mul3)
-            c.line("      const real a%d = kaok ? wr[%d + grp] : 0.0f;", st, w);
-          else
-            c.line("      const real a%d = (kaok && %d + grp < %d) ? wr[%d + grp < %d ? %d + grp : %d] : 0.0f;", st, w,
-                   mul3, w, mul3, w, mul3 - 1);
-        }
-        c.line("      const real* gr = g + (i64)brow * %d + %d;", s.out, q.out_off);
+        c.line("      const real* wr = wt + %d + (i64)(kaok ? ka : %d) * %d + grp * %d;", q.w_off, Ktot - 1, mul3,
+               quarter);
+        c.line("      const real* gr = g + (i64)brow * %d + %d + grp * %d;", s.out, q.out_off, quarter * d3);
         c.line("      const real* yr = y + (i64)brow * %d + %d;", s.in2, q.y_off);
         for (int v = 0; v < m2; ++v)
           for (int j : js) c.line("      const real y%d_%d = yr[%d];", v, j, v * q.d2 + j);
         for (int v = 0; v < m2; ++v)
           for (int j : js) c.line("      real gp%d_%d = 0;", v, j);
-        for (int k = 0; k < d3; ++k) {
-          bool any = false;
-          for (const auto& t : q.terms) any = any || t.k == k;
-          if (!any) continue;
-          c.line("      {");
-          c.line("        floatx4 dz = (floatx4)(0.0f);");
-          for (int st = 0; st < steps; ++st) {
-            const int w = 4 * st;
-            if (w + 3 < mul3)
-              c.line("        dz = mfma16(a%d, gr[(%d + grp) * %d + %d], dz);", st, w, d3, k);
-            else
-              c.line("        dz = mfma16(a%d, gr[(%d + grp < %d ? %d + grp : %d) * %d + %d], dz);", st, w, mul3, w,
-                     mul3 - 1, d3, k);
-          }
-          for (int r = 0; r < 4; ++r) {
-            const int v = r % m2, qd = r / m2;
-            for (const auto& t : q.terms) {
-              if (t.k != k) continue;
-              c.line("        gxa%d_%d = FMA(%s * y%d_%d, dz[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, r,
-                     qd, t.i);
-              c.line("        gp%d_%d = FMA(%s * x%d_%d, dz[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, r, v,
-                     t.j);
-            }
+        for (int k = 0; k < d3; ++k) c.line("      floatx4 dz%d = (floatx4)(0.0f);", k);
+        if (vec) {
+          // Chunks of 16 w: the seed rows of the 16 batch rows and the W rows
+          // of the 16 K indices go through LDS, read from HBM / L2 with
+          // consecutive lanes on consecutive addresses; within a chunk lane
+          // group grp takes w = 4 ss + grp.
+          const int gw = 16 * d3;  // floats of one batch row per chunk
+          c.line("      #pragma unroll 1");
+          c.line("      for (int c0 = 0; c0 < %d; c0 += 16) {", mul3);
+          c.line("        const float4* gg = (const float4*)(g + %d + c0 * %d);", q.out_off, d3);
+          c.line("        for (int idx = lane; idx < %d; idx += 64) {", 16 * gw / 4);
+          c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
+          c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
+          c.line("          const float4 v = gg[(i64)rr * %d + e];", s.out / 4);
+          c.line("          real* dst = &gs[wave][r][e * 4];");
+          c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
+          c.line("        }");
+          c.line("        {");
+          c.line("          const int r = lane >> 2, e = lane & 3, kr = kt * 16 + r;");
+          c.line("          const float4 v = kr < %d ? *(const float4*)(wt + %d + (i64)kr * %d + c0 + e * 4)"
+                 " : make_float4(0.0f, 0.0f, 0.0f, 0.0f);", Ktot, q.w_off, mul3);
+          c.line("          real* dst = &wsh[wave][r][e * 4];");
+          c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
+          c.line("        }");
+          c.line("        const real* gl = &gs[wave][c16][0];");
+          c.line("        const real* al = &wsh[wave][c16][0];");
+          for (int ss = 0; ss < 4; ++ss) {
+            c.line("        {");
+            c.line("          const int wl = %d + grp;", 4 * ss);
+            c.line("          const real a = al[wl];");
+            for (int k = 0; k < d3; ++k) c.line("          dz%d = mfma16(a, gl[wl * %d + %d], dz%d);", k, d3, k, k);
+            c.line("        }");
           }
           c.line("      }");
+        } else {
+          c.line("      #pragma unroll 4");
+          c.line("      for (int s = 0; s < %d; ++s) {", quarter);
+          c.line("        const int w = grp * %d + s;", quarter);
+          c.line("        const bool wok = w < %d;", mul3);
+          c.line("        const int sc = wok ? s : %d - grp * %d;", mul3 - 1, quarter);
+          c.line("        const real a = (kaok && wok) ? wr[sc] : 0.0f;");
+          for (int k = 0; k < d3; ++k) c.line("        dz%d = mfma16(a, gr[sc * %d + %d], dz%d);", k, d3, k, k);
+          c.line("      }");
+        }
+        for (int r = 0; r < 4; ++r) {
+          const int v = r % m2, qd = r / m2;
+          for (const auto& t : q.terms) {
+            c.line("      gxa%d_%d = FMA(%s * y%d_%d, dz%d[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, t.k, r,
+                   qd, t.i);
+            c.line("      gp%d_%d = FMA(%s * x%d_%d, dz%d[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, t.k, r, v,
+                   t.j);
+          }
         }
         // Sum over the four lane groups that share a batch row.
         for (int v = 0; v < m2; ++v)
@@ -553,9 +659,27 @@ std::string emit_backward_w(const UvwSpec& s) {
     c.line("  }");
   }
   c.line("}");
-  // gw[i] = sum over chunks of part[chunk][i], for the covered entries.
+  // gw[i] = sum over chunks of part[chunk][i], in two passes: kReduceGroups
+  // groups of chunks in parallel, then the group sums, for covered entries.
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w_reduce(");
-  c.line("    const real* __restrict__ part, real* __restrict__ gw, int chunks) {");
+  c.line("    const real* __restrict__ part, real* __restrict__ part2, int chunks) {");
+  c.line("  const int i = blockIdx.x * 256 + threadIdx.x;");
+  c.line("  if (i >= %d) return;", s.wnum);
+  c.line("  const int per = (chunks + %d) / %d;", kReduceGroups - 1, kReduceGroups);
+  c.line("  const int n0 = blockIdx.y * per, n1 = n0 + per < chunks ? n0 + per : chunks;");
+  c.line("  real a0 = 0, a1 = 0, a2 = 0, a3 = 0;");
+  c.line("  int n = n0;");
+  c.line("  for (; n + 3 < n1; n += 4) {");
+  c.line("    a0 += part[(i64)n * %d + i];", s.wnum);
+  c.line("    a1 += part[(i64)(n + 1) * %d + i];", s.wnum);
+  c.line("    a2 += part[(i64)(n + 2) * %d + i];", s.wnum);
+  c.line("    a3 += part[(i64)(n + 3) * %d + i];", s.wnum);
+  c.line("  }");
+  c.line("  for (; n < n1; ++n) a0 += part[(i64)n * %d + i];", s.wnum);
+  c.line("  part2[(i64)blockIdx.y * %d + i] = (a0 + a1) + (a2 + a3);", s.wnum);
+  c.line("}");
+  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w_final(");
+  c.line("    const real* __restrict__ part2, real* __restrict__ gw) {");
   c.line("  const int i = blockIdx.x * 256 + threadIdx.x;");
   c.line("  if (i >= %d) return;", s.wnum);
   std::string covered;
@@ -566,7 +690,7 @@ std::string emit_backward_w(const UvwSpec& s) {
   }
   c.line("  if (!(%s)) return;", covered.c_str());
   c.line("  real acc = 0;");
-  c.line("  for (int n = 0; n < chunks; ++n) acc += part[(i64)n * %d + i];", s.wnum);
+  c.line("  for (int n = 0; n < %d; ++n) acc += part2[(i64)n * %d + i];", kReduceGroups, s.wnum);
   c.line("  gw[i] = acc;");
   c.line("}");
   return c.s.str();
@@ -618,7 +742,8 @@ int64_t chunks_for(int64_t rows) { return (rows + kChunkRows - 1) / kChunkRows; 
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 size_t gw_part_bytes(const UvwPlan& p, int64_t rows) {
-  return align256((size_t)chunks_for(rows) * (size_t)p.spec.wnum * sizeof(float));
+  return align256((size_t)chunks_for(rows) * (size_t)p.spec.wnum * sizeof(float)) +
+         align256((size_t)kReduceGroups * (size_t)p.spec.wnum * sizeof(float));
 }
 size_t gy_part_bytes(const UvwPlan& p, int64_t rows) {
   return align256((size_t)p.gy_slots * (size_t)rows * (size_t)p.spec.in2 * sizeof(float));
@@ -732,7 +857,7 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
     hipStream_t s = (hipStream_t)stream;
     int B = (int)rows;
     const size_t need = gw_part_bytes(plan, rows) + gy_part_bytes(plan, rows);
-    if (rows > 0 && (gx || gy || gw) && (!workspace || workspace_bytes < need))
+    if ((((gx || gy) && rows > 0) || gw) && (!workspace || workspace_bytes < need))
       fail("luna_uvw_bwd: workspace too small");
     char* ws = (char*)workspace;
     void* gw_part = ws;
@@ -758,9 +883,13 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
                dim3((unsigned)((chunks + 3) / 4), (unsigned)plan.spec.paths.size()), dim3(256), s, args);
       }
       int n = (int)chunks;
-      void* args[] = {&gw_part, &gw, &n};
+      void* part2 = (char*)gw_part + align256((size_t)chunks * (size_t)plan.spec.wnum * sizeof(float));
+      void* args[] = {&gw_part, &part2, &n};
       launch("uvw_bwd_w_reduce", function_for(module, "luna_uvw_bwd_w_reduce"),
-             dim3((unsigned)((plan.spec.wnum + 255) / 256)), dim3(256), s, args);
+             dim3((unsigned)((plan.spec.wnum + 255) / 256), kReduceGroups), dim3(256), s, args);
+      void* args2[] = {&part2, &gw};
+      launch("uvw_bwd_w_final", function_for(module, "luna_uvw_bwd_w_final"),
+             dim3((unsigned)((plan.spec.wnum + 255) / 256)), dim3(256), s, args2);
     }
   });
 }
