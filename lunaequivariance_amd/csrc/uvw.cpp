@@ -403,12 +403,15 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       if (u.phase == phase)
         for (int p : u.paths)
           if (staged_seeds(s, s.paths[p])) stage_d3 = std::max(stage_d3, s.paths[p].d3);
+    // The four waves of a workgroup take four K tiles of one input block for
+    // the same 16 batch rows and share the staged seed rows.
     if (stage_d3) {
-      c.line("  __shared__ real gs[4][16][%d];", 16 * stage_d3 + 1);
+      c.line("  __shared__ real gs[2][16][%d];", 16 * stage_d3 + 1);
       c.line("  __shared__ real wsh[4][16][17];");
+      c.line("  int chunk = 0;");
     }
     c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
-    c.line("  const int b0 = (blockIdx.x * 4 + wave) * 16;");
+    c.line("  const int b0 = blockIdx.x * 16;");
     c.line("  if (b0 >= B) return;");
     c.line("  const bool rok = b0 + c16 < B;");
     c.line("  const int brow = rok ? b0 + c16 : B - 1;");
@@ -425,8 +428,10 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
         for (int v = 0; v < m2; ++v)
           for (int j : term_js(q)) cols[q.y_off + v * q.d2 + j] = "gc" + std::to_string(q.y_off + v * q.d2 + j);
       }
-      c.line("  if (unit < %d) {", kts);
-      c.line("    const int kt = unit;");
+      c.line("  if (unit == 0)");
+      c.line("  for (int kt0 = 0; kt0 < %d; kt0 += 4) {", kts);
+      c.line("    const bool tok = kt0 + wave < %d;", kts);
+      c.line("    const int kt = tok ? kt0 + wave : %d;", kts - 1);
       c.line("    const int ka = kt * 16 + c16;");  // A operand row (K index) of this lane
       c.line("    const bool kaok = ka < %d;", Ktot);
       c.line("    const int kb = kt * 16 + 4 * grp;");  // first of this lane's four D rows
@@ -481,11 +486,12 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
           c.line("      #pragma unroll 1");
           c.line("      for (int c0 = 0; c0 < %d; c0 += 16) {", mul3);
           c.line("        const float4* gg = (const float4*)(g + %d + c0 * %d);", q.out_off, d3);
-          c.line("        for (int idx = lane; idx < %d; idx += 64) {", 16 * gw / 4);
+          c.line("        real (*gsb)[%d] = gs[chunk & 1];", 16 * stage_d3 + 1);
+          c.line("        for (int idx = threadIdx.x; idx < %d; idx += 256) {", 16 * gw / 4);
           c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
           c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
           c.line("          const float4 v = gg[(i64)rr * %d + e];", s.out / 4);
-          c.line("          real* dst = &gs[wave][r][e * 4];");
+          c.line("          real* dst = &gsb[r][e * 4];");
           c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
           c.line("        }");
           c.line("        {");
@@ -495,7 +501,9 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
           c.line("          real* dst = &wsh[wave][r][e * 4];");
           c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
           c.line("        }");
-          c.line("        const real* gl = &gs[wave][c16][0];");
+          c.line("        __syncthreads();");
+          c.line("        ++chunk;");
+          c.line("        const real* gl = &gsb[c16][0];");
           c.line("        const real* al = &wsh[wave][c16][0];");
           for (int ss = 0; ss < 4; ++ss) {
             c.line("        {");
@@ -533,7 +541,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
           }
         c.line("    }");
       }
-      c.line("    if (rok) {");
+      c.line("    if (rok && tok) {");
       c.line("      real* gq = gx + (i64)brow * %d + %d;", s.in1, head.x_off);
       for (int qd = 0; qd < nq; ++qd) {
         const int r = qd * m2;
@@ -543,14 +551,13 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
           c.line("        gq[ur * %d + %d] %s gxa%d_%d;", d1, i, un.accumulate ? "+=" : "=", qd, i);
         c.line("      }");
       }
-      c.line("      if (grp == 0) {");
+      c.line("      if (grp == 0 && tok) {");
       c.line("        real* pr = part + ((i64)(%d + kt) * B + brow) * %d;", un.slot_base, s.in2);
       for (const auto& kv : cols) c.line("        pr[%d] = %s;", kv.first, kv.second.c_str());
       c.line("      }");
       c.line("    }");
-      c.line("    return;");
       c.line("  }");
-      c.line("  unit -= %d;", kts);
+      c.line("  unit -= 1;");
     }
     c.line("}");
   }
@@ -784,12 +791,12 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     for (Unit& u : p.bwd_units) {
       u.slot_base = p.gy_slots;
       p.gy_slots += ktiles16(p.spec.paths[u.paths[0]]);
-      p.bwd_phase_tiles[u.phase] += ktiles16(p.spec.paths[u.paths[0]]);
+      p.bwd_phase_tiles[u.phase] += 1;
     }
     for (int t : p.fwd_phase_tiles)
       if (t > 65535) fail("uvw: too many output tiles for one launch");
     for (int t : p.bwd_phase_tiles)
-      if (t > 65535) fail("uvw: too many K tiles for one launch");
+      if (t > 65535) fail("uvw: too many input blocks for one launch");
     p.out_needs_zero = out_collision || !covers(outs, p.spec.out);
     p.gx_needs_zero = gx_collision || !covers(xs, p.spec.in1);
     p.gy_needs_zero = false;  // the gy reduction writes every column
@@ -868,7 +875,7 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
       for (int phase = 0; phase < plan.bwd_phases; ++phase) {
         void* args[] = {&x, &y, &weight, &g, &gx, &gy_part, &B};
         launch("uvw_bwd_xy", function_for(module, "luna_uvw_bwd_xy_p" + std::to_string(phase)),
-               dim3(row_blocks(rows, 16), (unsigned)plan.bwd_phase_tiles[phase]), dim3(256), s, args);
+               dim3((unsigned)((rows + 15) / 16), (unsigned)plan.bwd_phase_tiles[phase]), dim3(256), s, args);
       }
       void* args[] = {&gy_part, &gy, &B};
       launch("uvw_bwd_gy", function_for(module, "luna_uvw_bwd_gy"), dim3((unsigned)((rows + 255) / 256)), dim3(256),
