@@ -224,14 +224,17 @@ def bench_uvw(args):
     ms = elapsed * 1000 / args.steps
     sum_d3 = sum(2 * a[k].ir.l + 1 for _, _, k, _, _ in instructions)
     gemm_flops = 2.0 * rows * sum_d3 * 64 * 64
-    flops = {"uvw_fwd": gemm_flops, "uvw_bwd_xy": gemm_flops, "uvw_bwd_w": gemm_flops / len(instructions)}
+    flops = {"uvw_fwd": gemm_flops, "uvw_bwd_xy": gemm_flops, "uvw_bwd_w": gemm_flops}
     per_kernel = {}
     for name, (count, total, low, high) in kernels.items():
         entry = {"launches": count, "avg_ms": round(total / count, 4)}
         if name in flops:
             entry["tflops"] = round(flops[name] / (total / count / 1000) / 1e12, 2)
         per_kernel[name] = entry
-    dominant = max(("uvw_fwd", "uvw_bwd_xy"), key=lambda n: kernels[n][1])
+    dominant = max(("uvw_fwd", "uvw_bwd_xy", "uvw_bwd_w"), key=lambda n: kernels[n][1])
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_uvw(ir, sh, instructions, x, y, w, g)
     achieved = per_kernel[dominant]["tflops"]
     print(json.dumps({
         "metric": "UVW shared-weight TP rows/s fwd+bwd", "value": round(rows / (ms / 1000), 1), "unit": "rows/s",
@@ -242,8 +245,32 @@ def bench_uvw(args):
                    "rows": rows, "weight_numel": tp.weight_numel, "parallelism": "single GPU"},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
-        "kernels": per_kernel, "cpu_baseline": None,
+        "kernels": per_kernel, "cpu_baseline": cpu,
     }))
+
+
+def cpu_baseline_uvw(ir, sh, instructions, x, y, w, g, sample=20000):
+    """The oracle's torch restatement of the UVW product, fp32, fwd+bwd, on the
+    first ``sample`` rows, timed on this host's cores."""
+    import torch
+
+    from oracle.uvw import uvw_tensor_product
+
+    xs = x.detach()[:sample].cpu().clone().requires_grad_()
+    ys = y.detach()[:sample].cpu().clone().requires_grad_()
+    ws = w.detach().cpu().clone().requires_grad_()
+    gs = g[:sample].cpu()
+    times = []
+    for repeat in range(4):
+        start = time.perf_counter()
+        out = uvw_tensor_product(ir, sh, ir, instructions, xs, ys, ws)
+        torch.autograd.grad(out, (xs, ys, ws), gs)
+        times.append(time.perf_counter() - start)
+    timed = times[1:]
+    return {"value": round(sample / statistics.median(timed), 1), "unit": "rows/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {sample} of {x.shape[0]} rows, fwd+bwd, median of {len(timed)} after 1 warm-up, "
+                      f"float32"}
 
 
 def measured_traffic(config, dtype, kernel):
