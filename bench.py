@@ -94,6 +94,13 @@ def main():
     src, dst, _pos, vec, _box = periodic_radius_graph(N, 0.1, 5.0, seed=0, device=device)
     E = src.numel()
     graph = conv.create_graph(src, dst, N)
+    graph_ms = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        conv.create_graph(src, dst, N)
+        torch.cuda.synchronize()
+        graph_ms.append((time.perf_counter() - start) * 1000.0)
     fan_in = len(instructions)
     x = torch.randn(N, conv.irreps_in1.dim, device=device, dtype=dtype, requires_grad=True)
     y = spherical_harmonics(3, vec).to(dtype).requires_grad_()
@@ -171,6 +178,7 @@ def main():
                                + (", fwd+bwd+double-bwd(gy)" if cfg["double_backward"] else ", fwd+bwd"),
                    "num_nodes": N, "num_edges": E, "channels": cfg["channels"],
                    "weight_numel": conv.weight_numel, "parallelism": "single GPU"},
+        "graph_build_ms": round(statistics.median(graph_ms), 3),
         "step_algorithmic_gb": round(step_bytes / 1e9, 3),
         "step_hbm_frac": round(step_bytes / (ms_per_step / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)
         if not cfg["double_backward"] else None,

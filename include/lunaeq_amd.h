@@ -172,6 +172,43 @@ int luna_uvw_bwd(const LunaUvwPlan* plan, const void* x, const void* y, const vo
                  const void* g, void* gx, void* gy, void* gw, void* workspace,
                  size_t workspace_bytes, int64_t rows, LunaStream stream);
 
+/* ------------------------------------------------------------------------ */
+/* Graph tables on the GPU.                                                  */
+
+/*
+ * status[0..3] (device int64) <- min index over src and dst, max index, 1 if
+ * dst descends anywhere else 0, 0.  index_bits is 32 or 64 (src and dst share
+ * it).  The caller reads status back to validate.
+ * replaces: graph_bounds of the reference's topology extension
+ * (src/lunatp/utils/graph.py:806-837, called from src/lunatp/graph.py:77).
+ */
+int luna_graph_bounds(const void* src, const void* dst, int index_bits, int64_t num_edges, int64_t* status,
+                      LunaStream stream);
+
+/* Bytes of device workspace luna_graph_build needs. */
+int luna_graph_workspace(int64_t num_nodes, int64_t num_edges, size_t* bytes);
+
+/*
+ * Every table of a validated, dst-sorted graph (int32):
+ *   src32, dst32 [E]; dst_rowptr, src_rowptr [N+1]; edge_ids_by_src [E]
+ *   (stable by source); edge_ids_by_dst [E]; node_order, source_node_order [N]
+ *   (descending degree, ties by node id); node_tiers [3]; seg_rowptr [N+1];
+ *   seg_nodes, seg_begin, seg_end, seg_order with room for N + E/32 + 1
+ *   segments, of which seg_rowptr[N] are real (the others are unspecified).
+ * replaces: make_graph_tables of the reference's topology extension
+ * (src/lunatp/utils/graph.py:142-846, called from src/lunatp/graph.py:106).
+ */
+int luna_graph_build(const void* src, const void* dst, int index_bits, int64_t num_nodes, int64_t num_edges,
+                     int32_t* src32, int32_t* dst32, int32_t* dst_rowptr, int32_t* src_rowptr,
+                     int32_t* edge_ids_by_src, int32_t* edge_ids_by_dst, int32_t* node_order,
+                     int32_t* source_node_order, int32_t* node_tiers, int32_t* seg_rowptr, int32_t* seg_nodes,
+                     int32_t* seg_begin, int32_t* seg_end, int32_t* seg_order, void* workspace,
+                     size_t workspace_bytes, LunaStream stream);
+
+/* Compile (or load from cache_dir) the graph kernels without touching a device;
+ * also sets the cache directory the graph kernels use afterwards. */
+int luna_graph_precompile(const char* cache_dir);
+
 /*
  * Measurement hook (no counterpart in the reference): while enabled, every
  * launch is bracketed by HIP events on its stream.  luna_profile_collect waits

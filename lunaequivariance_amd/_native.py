@@ -44,6 +44,11 @@ PROTOTYPES = {
     "luna_uvw_fwd": (ctypes.c_int, [_VP] * 5 + [_I64, _VP]),
     "luna_uvw_bwd_workspace": (ctypes.c_int, [_VP, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_uvw_bwd": (ctypes.c_int, [_VP] * 9 + [ctypes.c_size_t, _I64, _VP]),
+    "luna_graph_bounds": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _VP, _VP]),
+    "luna_graph_workspace": (ctypes.c_int, [_I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
+    "luna_graph_build": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _I64] + [_VP] * 15
+                         + [ctypes.c_size_t, _VP]),
+    "luna_graph_precompile": (ctypes.c_int, [ctypes.c_char_p]),
     "luna_profile_enable": (ctypes.c_int, [ctypes.c_int]),
     "luna_profile_collect": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t,
                                              ctypes.POINTER(ctypes.c_size_t)]),

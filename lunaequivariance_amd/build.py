@@ -13,7 +13,7 @@ import subprocess
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
-SOURCES = ["common.cpp", "uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp", "uvw.cpp"]
+SOURCES = ["common.cpp", "uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp", "uvw.cpp", "graph.cpp"]
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wno-format-security",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -90,7 +90,10 @@ def uvw_operators():
 
 
 def precompile() -> int:
-    count = 0
+    from . import _native
+
+    _native.check(_native.lib().luna_graph_precompile(_native.cache_dir().encode()), "luna_graph_precompile")
+    count = 1
     for op in standard_operators() + uvw_operators():
         op.plan.precompile()
         count += 1

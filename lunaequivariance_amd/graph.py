@@ -1,10 +1,12 @@
 """Graph validation and CSR tables shared by the convolution kernels.
 
 Restates ``make_graph`` / ``LunaTPGraph`` (``src/lunatp/graph.py:17-141``) and
-``make_source_segments`` (``src/lunatp/uvu_conv/graph.py:38-99``).  The tables
-are built with torch operations on the inputs' device; the edge permutation
-by source is a *stable* sort, so equal sources keep destination order and
-every table is deterministic.
+``make_source_segments`` (``src/lunatp/uvu_conv/graph.py:38-99``).  Tables of
+GPU inputs are built by the HIP kernels of the C-ABI library (radix sort,
+scans, binary-search row pointers); tables of CPU inputs with torch
+operations.  Both orderings are *stable* (equal sources keep destination
+order, equal degrees keep node order), so every table is deterministic and
+the two builders agree exactly.
 
 Tables (int32):
   src, dst           copies of the inputs (the graph owns them)
@@ -122,6 +124,8 @@ def make_graph(src: torch.Tensor, dst: torch.Tensor, num_nodes: int | None = Non
     if num_nodes is not None and not isinstance(num_nodes, int):
         num_nodes = index(num_nodes)
     num_edges = src.numel()
+    if src.is_cuda:
+        return _make_graph_device(src, dst, num_nodes)
     required = 0
     if num_edges:
         src_min, src_max = torch.aminmax(src)
@@ -133,15 +137,7 @@ def make_graph(src: torch.Tensor, dst: torch.Tensor, num_nodes: int | None = Non
         if num_edges > 1 and bool((dst[1:] < dst[:-1]).any()):
             raise ValueError(
                 "dst must be sorted in ascending order; src and edge data must follow the same order.")
-    if num_nodes is None:
-        num_nodes = required
-    if num_nodes < required:
-        raise ValueError(
-            f"num_nodes={num_nodes} must be nonnegative and at least {required} for the supplied indices.")
-    if num_nodes >= (1 << 31):
-        raise OverflowError("graph node count exceeds signed int32 capacity.")
-    if num_edges >= (1 << 31) - 1:
-        raise OverflowError("graph edge count exceeds signed int32 capacity.")
+    num_nodes = _check_nodes(num_nodes, required, num_edges)
 
     device = src.device
     i32 = torch.int32
@@ -175,6 +171,80 @@ def make_graph(src: torch.Tensor, dst: torch.Tensor, num_nodes: int | None = Non
         source_segments=make_source_segments(src_rowptr),
     )
     return graph
+
+
+def _check_nodes(num_nodes, required, num_edges):
+    if num_nodes is None:
+        num_nodes = required
+    if num_nodes < required:
+        raise ValueError(
+            f"num_nodes={num_nodes} must be nonnegative and at least {required} for the supplied indices.")
+    if num_nodes >= (1 << 31):
+        raise OverflowError("graph node count exceeds signed int32 capacity.")
+    if num_edges >= (1 << 31) - 1:
+        raise OverflowError("graph edge count exceeds signed int32 capacity.")
+    return num_nodes
+
+
+def _make_graph_device(src: torch.Tensor, dst: torch.Tensor, num_nodes) -> LunaTPGraph:
+    """Tables of a device graph from the HIP kernels of the C-ABI library
+    (``luna_graph_bounds`` / ``luna_graph_build``; the reference's topology
+    extension, ``src/lunatp/utils/graph.py:142-846``).  The indices are always
+    validated (one read-back of min, max and sortedness), also when
+    ``num_nodes`` is given, because every later kernel indexes with them."""
+    import ctypes
+
+    from . import _native
+
+    if src.dtype != dst.dtype:
+        dst = dst.to(src.dtype)
+    src, dst = src.contiguous(), dst.contiguous()
+    bits = 64 if src.dtype == torch.int64 else 32
+    num_edges = src.numel()
+    device = src.device
+    lib = _native.lib()
+    _native.check(lib.luna_graph_precompile(_native.cache_dir().encode()), "luna_graph_precompile")
+    stream = torch.cuda.current_stream(device).cuda_stream
+    required = 0
+    if num_edges:
+        status = torch.empty(4, dtype=torch.int64, device=device)
+        _native.check(lib.luna_graph_bounds(src.data_ptr(), dst.data_ptr(), bits, num_edges, status.data_ptr(),
+                                            stream), "luna_graph_bounds")
+        low, high, unsorted, _ = status.tolist()
+        if low < 0:
+            raise ValueError("graph indices must be nonnegative.")
+        if unsorted:
+            raise ValueError(
+                "dst must be sorted in ascending order; src and edge data must follow the same order.")
+        required = high + 1
+    num_nodes = _check_nodes(num_nodes, required, num_edges)
+    i32 = torch.int32
+    E, N = num_edges, num_nodes
+    cap = N + E // SOURCE_SEGMENT_EDGES + 1
+    new = lambda n: torch.empty(n, dtype=i32, device=device)
+    t = {name: new(n) for name, n in (
+        ("src", E), ("dst", E), ("dst_rowptr", N + 1), ("src_rowptr", N + 1), ("edge_ids_by_src", E),
+        ("edge_ids_by_dst", E), ("node_order", N), ("source_node_order", N), ("node_tiers", 3),
+        ("seg_rowptr", N + 1), ("seg_nodes", cap), ("seg_begin", cap), ("seg_end", cap), ("seg_order", cap))}
+    size = ctypes.c_size_t()
+    _native.check(lib.luna_graph_workspace(N, E, ctypes.byref(size)), "luna_graph_workspace")
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+    order = ("src", "dst", "dst_rowptr", "src_rowptr", "edge_ids_by_src", "edge_ids_by_dst", "node_order",
+             "source_node_order", "node_tiers", "seg_rowptr", "seg_nodes", "seg_begin", "seg_end", "seg_order")
+    _native.check(lib.luna_graph_build(
+        src.data_ptr() if E else None, dst.data_ptr() if E else None, bits, N, E,
+        *(t[name].data_ptr() if t[name].numel() else None for name in order),
+        workspace.data_ptr(), size.value, stream), "luna_graph_build")
+    segments = int(t["seg_rowptr"][N].item()) if N else 0
+    return LunaTPGraph(
+        src=t["src"], dst=t["dst"], num_nodes=N,
+        dst_rowptr=t["dst_rowptr"], src_rowptr=t["src_rowptr"],
+        edge_ids_by_src=t["edge_ids_by_src"], edge_ids_by_dst=t["edge_ids_by_dst"],
+        node_order=t["node_order"], source_node_order=t["source_node_order"], node_tiers=t["node_tiers"],
+        source_segments=SourceSegmentTables(
+            t["seg_nodes"][:segments], t["seg_begin"][:segments], t["seg_end"][:segments], t["seg_rowptr"],
+            t["seg_order"][:segments]),
+    )
 
 
 __all__ = ["LunaTPGraph", "SourceSegmentTables", "make_graph", "make_source_segments",
