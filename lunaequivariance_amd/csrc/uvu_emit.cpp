@@ -832,24 +832,40 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
       }
     }
   }
-  // One thread per edge; every output column is a fixed sum of partial columns.
+  // 256 edges per workgroup.  Each partial slot's rows of those edges are one
+  // contiguous run (PART_W values per edge): they are copied into LDS with
+  // consecutive threads on consecutive addresses, then every thread adds its
+  // edge's columns; the gy rows leave through LDS the same way.
+  std::map<int, std::vector<std::pair<int, int>>> by_slot;  // slot -> (partial column, output column)
+  for (int col = 0; col < pw; ++col)
+    for (const auto& sc : writers[col]) by_slot[sc.first].push_back({sc.second, col});
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_bwd_reduce(");
   c.line("    const real* __restrict__ part, real* __restrict__ gy, real* __restrict__ genv, i64 E) {");
-  c.line("  const i64 e = (i64)blockIdx.x * 256 + threadIdx.x;");
-  c.line("  if (e >= E) return;");
-  for (int col = 0; col < pw; ++col) {
-    std::string sum;
-    for (const auto& sc : writers[col]) {
-      char term[128];
-      std::snprintf(term, sizeof(term), "part[((i64)%d * E + e) * PART_W + %d]", sc.first, sc.second);
-      sum += (sum.empty() ? "" : " + ") + std::string(term);
-    }
-    if (sum.empty()) sum = "(real)0";
-    if (col < spec.in2)
-      c.line("  if (gy) gy[e * IN2 + %d] = %s;", col, sum.c_str());
-    else
-      c.line("  if (genv) genv[e] = %s;", sum.c_str());
+  c.line("  __shared__ real tile[256 * PART_W];");
+  c.line("  const int t = threadIdx.x;");
+  c.line("  const i64 e0 = (i64)blockIdx.x * 256;");
+  c.line("  const int n = E - e0 < 256 ? (int)(E - e0) : 256;");
+  for (int col = 0; col < pw; ++col) c.line("  real acc%d = 0;", col);
+  for (const auto& kv : by_slot) {
+    c.line("  {");
+    c.line("    const real* src = part + ((i64)%d * E + e0) * PART_W;", kv.first);
+    c.line("    for (int i = t; i < n * (int)PART_W; i += 256) tile[i] = src[i];");
+    c.line("    __syncthreads();");
+    c.line("    if (t < n) {");
+    for (const auto& pc : kv.second) c.line("      acc%d += tile[t * PART_W + %d];", pc.second, pc.first);
+    c.line("    }");
+    c.line("    __syncthreads();");
+    c.line("  }");
   }
+  c.line("  if (gy) {");
+  c.line("    if (t < n) {");
+  for (int col = 0; col < spec.in2; ++col) c.line("      tile[t * IN2 + %d] = acc%d;", col, col);
+  c.line("    }");
+  c.line("    __syncthreads();");
+  c.line("    real* dst = gy + e0 * IN2;");
+  c.line("    for (int i = t; i < n * (int)IN2; i += 256) dst[i] = tile[i];");
+  c.line("  }");
+  if (env) c.line("  if (genv && t < n) genv[e0 + t] = acc%d;", spec.in2);
   c.line("}");
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_fill(real* __restrict__ p, i64 n) {");
   c.line("  const i64 i = (i64)blockIdx.x * 256 + threadIdx.x;");
