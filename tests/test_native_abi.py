@@ -135,3 +135,21 @@ def test_fp64_backward_splits_large_groups():
     f64 = op_for(channels=128, lmax=3, dtype=torch.float64).plan.info
     assert f32.gy_parts == 4 * 2
     assert f64.gy_parts == 2 + 3 * 2 * 2
+
+
+def test_graph_entry_points_check_arguments():
+    """The graph builder's argument checks fail before any device work."""
+    lib = _native.lib()
+    size = ctypes.c_size_t()
+    _native.check(lib.luna_graph_workspace(20000, 1047038, ctypes.byref(size)), "workspace")
+    assert size.value > 20000 * 4
+    with pytest.raises(RuntimeError, match="negative"):
+        _native.check(lib.luna_graph_workspace(-1, 5, ctypes.byref(size)), "workspace")
+    with pytest.raises(RuntimeError, match="int32"):
+        _native.check(lib.luna_graph_workspace(1 << 31, 5, ctypes.byref(size)), "workspace")
+    with pytest.raises(RuntimeError, match="index_bits"):
+        _native.check(lib.luna_graph_bounds(None, None, 16, 0, None, None), "bounds")
+    with pytest.raises(RuntimeError, match="null"):
+        _native.check(lib.luna_graph_bounds(None, None, 32, 4, None, None), "bounds")
+    with pytest.raises(RuntimeError, match="null table"):
+        _native.check(lib.luna_graph_build(None, None, 32, 4, 0, *([None] * 15), 0, None), "build")
