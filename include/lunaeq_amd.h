@@ -173,6 +173,62 @@ int luna_uvw_bwd(const LunaUvwPlan* plan, const void* x, const void* y, const vo
                  size_t workspace_bytes, int64_t rows, LunaStream stream);
 
 /* ------------------------------------------------------------------------ */
+/* UUU (channel-wise) tensor-product convolution.                            */
+
+typedef struct LunaUuuPlan LunaUuuPlan;
+
+/*
+ * Build a UUU convolution plan (the metadata of build_uuu_conv_metadata,
+ * src/lunatp/uuu_conv/kernels/utils.py:342-364, lowered by build_uuu_metadata,
+ * src/lunatp/uuu/kernels/utils.py:250-330):
+ *   "LUNAUUU1 <dtype_bits> <in1> <in2> <out> <weight_numel> <npaths> <l0_dim>"
+ *   then per path:
+ *   "<x_off> <y_off> <out_off> <w_off or -1 if unweighted> <channels> <d1> <d2>
+ *    <d3> <l0_col or -1> <nterms> (<i> <j> <k> <coefficient>)*nterms"
+ * A path reads x[s, x_off + u*d1 + i], y[e, y_off + u*d2 + j] and
+ * w[e, w_off + u] for each channel u < channels and writes
+ * out[t, out_off + u*d3 + k].  Coefficients include the path weight.
+ * replaces: LunaTPUUUConv / configure_uuu_conv (src/lunatp/interface.py:338-350,
+ * src/lunatp/uuu_conv/kernels/utils.py:116-199)
+ */
+int luna_uuu_plan_create(const char* spec, const char* cache_dir, LunaUuuPlan** plan);
+int luna_uuu_plan_destroy(LunaUuuPlan* plan);
+/* flags[0..3]: out, gx, gy, gw must be zero-filled by the caller (ranges no path covers). */
+int luna_uuu_plan_needs_zero(const LunaUuuPlan* plan, int32_t* flags);
+int luna_uuu_plan_precompile(LunaUuuPlan* plan);
+
+/*
+ * Forward: out[t] = sum over edges e with dst[e]==t of env[e] * msg[e]; l0 (may
+ * be NULL) receives the scalar-path messages before env, one column per
+ * channel.  Destination-owned over the dst CSR (src, dst_rowptr, node_order).
+ * replaces: run_uuu_conv at order 0 (src/lunatp/uuu_conv/kernels/utils.py:87-112,
+ * launched by launch_forward, src/lunatp/uuu_conv/kernels/traversal.py:2095)
+ */
+int luna_uuu_conv_fwd(const LunaUuuPlan* plan, const void* x, const void* y, const void* w,
+                      const void* env, const int32_t* src, const int32_t* dst_rowptr,
+                      const int32_t* node_order, void* out, void* l0, int64_t num_nodes,
+                      int64_t num_edges, LunaStream stream);
+
+/* Bytes of device workspace luna_uuu_conv_bwd needs (env-gradient partials; may be 0). */
+int luna_uuu_conv_bwd_workspace(const LunaUuuPlan* plan, int64_t num_nodes, int64_t num_edges,
+                                size_t* bytes);
+
+/*
+ * First-order backward for the seed g [N, out] (and gl0 [E, l0_dim] or NULL):
+ * gx [N, in1], gy [E, in2], gw [E, weight_numel], genv [E] (only with env);
+ * any output may be NULL.  Source-owned over the src CSR (src_rowptr,
+ * edge_ids_by_src, source_node_order) with dst[E] to find each edge's seed.
+ * replaces: run_uuu_conv at order 1 (src/lunatp/uuu_conv/kernels/utils.py:87-112,
+ * driven by run, src/lunatp/uuu_conv/kernels/traversal.py:1943-2092)
+ */
+int luna_uuu_conv_bwd(const LunaUuuPlan* plan, const void* x, const void* y, const void* w,
+                      const void* env, const void* g, const void* gl0, const int32_t* dst,
+                      const int32_t* src_rowptr, const int32_t* edge_ids_by_src,
+                      const int32_t* source_node_order, void* gx, void* gy, void* gw, void* genv,
+                      void* workspace, size_t workspace_bytes, int64_t num_nodes, int64_t num_edges,
+                      LunaStream stream);
+
+/* ------------------------------------------------------------------------ */
 /* Graph tables on the GPU.                                                  */
 
 /*

@@ -44,6 +44,14 @@ PROTOTYPES = {
     "luna_uvw_fwd": (ctypes.c_int, [_VP] * 5 + [_I64, _VP]),
     "luna_uvw_bwd_workspace": (ctypes.c_int, [_VP, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_uvw_bwd": (ctypes.c_int, [_VP] * 9 + [ctypes.c_size_t, _I64, _VP]),
+    "luna_uuu_plan_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_VP)]),
+    "luna_uuu_plan_destroy": (ctypes.c_int, [_VP]),
+    "luna_uuu_plan_needs_zero": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_int32)]),
+    "luna_uuu_plan_precompile": (ctypes.c_int, [_VP]),
+    "luna_uuu_conv_fwd": (ctypes.c_int, [_VP] + [_VP] * 4 + [_I32P] * 3 + [_VP, _VP, _I64, _I64, _VP]),
+    "luna_uuu_conv_bwd_workspace": (ctypes.c_int, [_VP, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
+    "luna_uuu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 4 + [_VP] * 5
+                          + [ctypes.c_size_t, _I64, _I64, _VP]),
     "luna_graph_bounds": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _VP, _VP]),
     "luna_graph_workspace": (ctypes.c_int, [_I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_graph_build": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _I64] + [_VP] * 15

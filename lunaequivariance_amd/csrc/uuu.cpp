@@ -1,0 +1,835 @@
+// UUU ("channel-wise") tensor-product convolution on gfx950.
+//
+// For a path p with C channels (mul_in1 = mul_in2 = mul_out = C) and an edge
+// e = (s -> t):
+//   msg_p[e, u, k] = a_p[e, u] * sum_{(i,j,k)} c_ijk x[s, xo + u*d1 + i] y[e, yo + u*d2 + j]
+//   out[t, oo + u*d3 + k] += env[e] * msg_p[e, u, k]
+// with a_p = w[e, wo + u] for weighted paths and 1 otherwise (e3nn's uuu
+// connection; src/lunatp/uuu/kernels/utils.py:250-330 lowers the paths and
+// src/lunatp/uuu_conv/interface.py:143-240 defines the convolution).
+//
+// Every operand of one channel u is private to that channel, so one lane owns
+// one channel and no value ever crosses lanes except in the sums over edges:
+//   forward  (destination-owned): a wave streams the in-edges of node t and
+//            keeps out[t] in registers; it gathers x[src] per edge;
+//   backward (source-owned): a wave streams the out-edges of node s
+//            (edge_ids_by_src), gathers g[dst] per edge, keeps gx[s] in
+//            registers and writes gy[e] and gw[e] straight from the lanes.
+// The source-owned backward needs no per-edge gx messages and no second
+// pass; the reference's backward traverses sources the same way
+// (src/lunatp/uuu_conv/interface.py:300-330).
+//
+// Channel counts below 64 would leave lanes idle, so a wave covers 64 / W
+// edges at once with W = the next power of two >= C: lane = sub * W + u, and
+// the per-node sums are completed across the sub-groups with lane exchanges.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <functional>
+#include <map>
+#include <memory>
+#include <set>
+#include <sstream>
+
+#include "../../include/lunaeq_amd.h"
+#include "common.h"
+
+namespace luna {
+namespace {
+
+struct UTerm {
+  int i, j, k;
+  double c;
+};
+
+struct UPath {
+  int x_off, y_off, out_off, w_off, ch, d1, d2, d3, l0_col;
+  std::vector<UTerm> terms;
+  int xb = -1, yb = -1, ob = -1;  // block ids
+};
+
+// A block of one operand: channels x d components starting at off.
+struct UBlock {
+  int off, d, ch;
+};
+
+struct USpec {
+  int bits = 32;
+  int in1 = 0, in2 = 0, out = 0, wnum = 0, l0 = 0;
+  std::vector<UPath> paths;
+  std::vector<UBlock> xblocks, yblocks, oblocks;
+};
+
+// One wave body: the paths a wave evaluates for one node and channel chunk.
+struct UGroup {
+  std::vector<int> paths;
+  int ch = 0, cw = 64, chunks = 1;
+  int phase = 0;                 // backward: launch order among groups sharing edge blocks
+  int genv_slot = 0;             // backward: first partial slot of env's gradient
+  std::set<int> xbs, ybs, obs;
+  std::set<int> gy_accumulate;   // backward: y blocks already written by an earlier phase
+};
+
+struct UuuPlan {
+  USpec spec;
+  std::vector<UGroup> fwd, bwd;
+  int bwd_phases = 0;
+  int genv_slots = 0;
+  bool out_zero = false, gx_zero = false, gy_zero = false, gw_zero = false;
+  ModuleCache kernels;
+};
+
+// Accumulated register estimates (32-bit registers) per wave body.
+constexpr int kForwardBudget = 96;
+constexpr int kBackwardBudget = 128;
+
+int read_int(std::istringstream& in, const char* what) {
+  long long value;
+  if (!(in >> value)) fail(std::string("uuu spec: expected integer for ") + what);
+  if (value < -1 || value > (1LL << 31) - 1) fail(std::string("uuu spec: value out of range for ") + what);
+  return (int)value;
+}
+
+// Block id of [off, off + ch*d) in `blocks`; distinct blocks must not overlap.
+int block_id(std::vector<UBlock>& blocks, int off, int d, int ch, const char* what) {
+  const long lo = off, hi = off + (long)ch * d;
+  for (size_t n = 0; n < blocks.size(); ++n) {
+    const UBlock& b = blocks[n];
+    if (b.off == off && b.d == d && b.ch == ch) return (int)n;
+    if (lo < b.off + (long)b.ch * b.d && b.off < hi)
+      fail(std::string("uuu spec: overlapping ") + what + " blocks of different shape");
+  }
+  blocks.push_back({off, d, ch});
+  return (int)blocks.size() - 1;
+}
+
+USpec parse(const std::string& text) {
+  std::istringstream in(text);
+  std::string magic;
+  in >> magic;
+  if (magic != "LUNAUUU1") fail("uuu spec: missing LUNAUUU1 header");
+  USpec s;
+  s.bits = read_int(in, "dtype");
+  if (s.bits != 32 && s.bits != 64) fail("uuu spec: dtype must be 32 or 64");
+  s.in1 = read_int(in, "in1");
+  s.in2 = read_int(in, "in2");
+  s.out = read_int(in, "out");
+  s.wnum = read_int(in, "weight_numel");
+  const int npaths = read_int(in, "npaths");
+  s.l0 = read_int(in, "l0_dim");
+  if (s.in1 < 0 || s.in2 < 0 || s.out < 0 || s.wnum < 0 || s.l0 < 0 || npaths < 0)
+    fail("uuu spec: negative dimension");
+  for (int n = 0; n < npaths; ++n) {
+    UPath p;
+    p.x_off = read_int(in, "x_off");
+    p.y_off = read_int(in, "y_off");
+    p.out_off = read_int(in, "out_off");
+    p.w_off = read_int(in, "w_off");
+    p.ch = read_int(in, "channels");
+    p.d1 = read_int(in, "d1");
+    p.d2 = read_int(in, "d2");
+    p.d3 = read_int(in, "d3");
+    p.l0_col = read_int(in, "l0_col");
+    const int nterms = read_int(in, "nterms");
+    if (p.ch <= 0) fail("uuu spec: UUU convolution requires positive channels for every path");
+    if (p.d1 <= 0 || p.d2 <= 0 || p.d3 <= 0 || nterms < 0) fail("uuu spec: bad path dimensions");
+    if (p.x_off < 0 || (long)p.x_off + (long)p.ch * p.d1 > s.in1) fail("uuu spec: input block outside in1_dim");
+    if (p.y_off < 0 || (long)p.y_off + (long)p.ch * p.d2 > s.in2) fail("uuu spec: edge block outside in2_dim");
+    if (p.out_off < 0 || (long)p.out_off + (long)p.ch * p.d3 > s.out)
+      fail("uuu spec: output block outside out_dim");
+    if (p.w_off >= 0 && (long)p.w_off + p.ch > s.wnum) fail("uuu spec: weight block outside weight_numel");
+    if (p.l0_col >= 0 && (p.d3 != 1 || (long)p.l0_col + p.ch > s.l0)) fail("uuu spec: l0 column outside l0_dim");
+    for (int t = 0; t < nterms; ++t) {
+      UTerm term;
+      term.i = read_int(in, "i");
+      term.j = read_int(in, "j");
+      term.k = read_int(in, "k");
+      std::string token;
+      in >> token;
+      char* end = nullptr;
+      term.c = std::strtod(token.c_str(), &end);
+      if (token.empty() || *end) fail("uuu spec: bad coefficient '" + token + "'");
+      if (term.i < 0 || term.i >= p.d1 || term.j < 0 || term.j >= p.d2 || term.k < 0 || term.k >= p.d3)
+        fail("uuu spec: coefficient index outside the path's irreps");
+      p.terms.push_back(term);
+    }
+    p.xb = block_id(s.xblocks, p.x_off, p.d1, p.ch, "input");
+    p.yb = block_id(s.yblocks, p.y_off, p.d2, p.ch, "edge");
+    p.ob = block_id(s.oblocks, p.out_off, p.d3, p.ch, "output");
+    s.paths.push_back(std::move(p));
+  }
+  // Weighted paths must own disjoint weight ranges (each writes its gradient).
+  std::vector<std::pair<int, int>> ws;
+  for (const UPath& p : s.paths)
+    if (p.w_off >= 0) ws.push_back({p.w_off, p.w_off + p.ch});
+  std::sort(ws.begin(), ws.end());
+  for (size_t n = 1; n < ws.size(); ++n)
+    if (ws[n].first < ws[n - 1].second) fail("uuu spec: weight ranges of two paths overlap");
+  return s;
+}
+
+int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v && p < 64) p *= 2;
+  return p;
+}
+
+void finish_group(UGroup& g, const USpec& s) {
+  g.ch = s.paths[g.paths[0]].ch;
+  g.cw = pow2_at_least(g.ch);
+  g.chunks = (g.ch + 63) / 64;
+  for (int p : g.paths) {
+    g.xbs.insert(s.paths[p].xb);
+    g.ybs.insert(s.paths[p].yb);
+    g.obs.insert(s.paths[p].ob);
+  }
+}
+
+int cost(const USpec& s, const std::vector<int>& paths, bool backward) {
+  std::set<int> xs, ys, os;
+  int weights = 0;
+  for (int p : paths) {
+    xs.insert(s.paths[p].xb);
+    ys.insert(s.paths[p].yb);
+    os.insert(s.paths[p].ob);
+    weights += s.paths[p].w_off >= 0;
+  }
+  int regs = weights;
+  for (int b : xs) regs += s.xblocks[b].d * (backward ? 2 : 1);
+  for (int b : ys) regs += s.yblocks[b].d * (backward ? 2 : 1);
+  for (int b : os) regs += s.oblocks[b].d;
+  return regs * (s.bits / 32);
+}
+
+// Forward: paths writing one output block stay together (plain stores, no
+// collisions); output blocks of one channel count are packed into a group
+// while its register estimate fits.
+std::vector<UGroup> forward_groups(const USpec& s) {
+  std::vector<std::vector<int>> units(s.oblocks.size());
+  for (int p = 0; p < (int)s.paths.size(); ++p) units[s.paths[p].ob].push_back(p);
+  std::vector<UGroup> groups;
+  std::map<int, int> open;  // channels -> index of the group being filled
+  for (const auto& unit : units) {
+    const int ch = s.paths[unit[0]].ch;
+    auto it = open.find(ch);
+    if (it != open.end()) {
+      std::vector<int> merged = groups[it->second].paths;
+      merged.insert(merged.end(), unit.begin(), unit.end());
+      if (cost(s, merged, false) <= kForwardBudget) {
+        groups[it->second].paths = merged;
+        continue;
+      }
+    }
+    UGroup g;
+    g.paths = unit;
+    groups.push_back(g);
+    open[ch] = (int)groups.size() - 1;
+  }
+  for (UGroup& g : groups) finish_group(g, s);
+  return groups;
+}
+
+// Backward: a group owns whole input blocks (gx stays in registers) and, when
+// it fits, whole connected sets of input and edge blocks (gy in registers).
+// A connected set over budget is cut by input block into groups of distinct
+// phases; a later phase adds its share of gy to what the earlier one wrote.
+std::vector<UGroup> backward_groups(const USpec& s, int* phases) {
+  const int nx = (int)s.xblocks.size();
+  std::vector<int> root(nx + s.yblocks.size());
+  for (size_t n = 0; n < root.size(); ++n) root[n] = (int)n;
+  std::function<int(int)> find = [&](int a) { return root[a] == a ? a : root[a] = find(root[a]); };
+  for (const UPath& p : s.paths) root[find(p.xb)] = find(nx + p.yb);
+  std::map<int, std::vector<int>> components;  // root -> input blocks, in order
+  std::vector<int> component_order;
+  for (int b = 0; b < nx; ++b) {
+    bool used = false;
+    for (const UPath& p : s.paths) used |= p.xb == b;
+    if (!used) continue;
+    const int r = find(b);
+    if (!components.count(r)) component_order.push_back(r);
+    components[r].push_back(b);
+  }
+  std::vector<UGroup> groups;
+  *phases = 0;
+  for (int r : component_order) {
+    std::vector<std::vector<int>> parts;  // paths per cut
+    std::vector<int> current;
+    for (int b : components[r]) {
+      std::vector<int> block;
+      for (int p = 0; p < (int)s.paths.size(); ++p)
+        if (s.paths[p].xb == b) block.push_back(p);
+      std::vector<int> merged = current;
+      merged.insert(merged.end(), block.begin(), block.end());
+      if (!current.empty() && cost(s, merged, true) > kBackwardBudget) {
+        parts.push_back(current);
+        current = block;
+      } else {
+        current = merged;
+      }
+    }
+    parts.push_back(current);
+    std::set<int> written;
+    for (size_t n = 0; n < parts.size(); ++n) {
+      UGroup g;
+      g.paths = parts[n];
+      std::sort(g.paths.begin(), g.paths.end());
+      g.phase = (int)n;
+      finish_group(g, s);
+      for (int b : g.ybs)
+        if (written.count(b)) g.gy_accumulate.insert(b);
+      written.insert(g.ybs.begin(), g.ybs.end());
+      groups.push_back(g);
+    }
+    *phases = std::max(*phases, (int)parts.size());
+  }
+  return groups;
+}
+
+bool covers(std::vector<std::pair<long, long>> ranges, long total) {
+  std::sort(ranges.begin(), ranges.end());
+  long at = 0;
+  for (const auto& r : ranges) {
+    if (r.first > at) return false;
+    at = std::max(at, r.second);
+  }
+  return at >= total;
+}
+
+// ---------------------------------------------------------------------------
+// Emission
+// ---------------------------------------------------------------------------
+
+struct Code {
+  std::ostringstream s;
+  template <typename... A>
+  __attribute__((format(printf, 2, 0))) void line(const char* fmt, A... args) {
+    const int size = std::snprintf(nullptr, 0, fmt, args...);
+    std::string buffer(size + 1, '\0');
+    std::snprintf(&buffer[0], buffer.size(), fmt, args...);
+    buffer.resize(size);
+    s << buffer << '\n';
+  }
+};
+
+std::string lit(double c, int bits) {
+  char b[48];
+  if (bits == 64)
+    std::snprintf(b, sizeof(b), "%.17e", c);
+  else
+    std::snprintf(b, sizeof(b), "%.9ef", (double)(float)c);
+  return b;
+}
+
+std::string prelude(const USpec& s) {
+  std::ostringstream o;
+  o << "typedef " << (s.bits == 64 ? "double" : "float") << " real;\n";
+  o << "typedef long long i64;\n";
+  o << "#define FMA(a, b, c) " << (s.bits == 64 ? "__builtin_fma" : "__builtin_fmaf") << "((a), (b), (c))\n";
+  o << "#define IN1 " << s.in1 << "LL\n#define IN2 " << s.in2 << "LL\n#define OUTD " << s.out
+    << "LL\n#define WNUM " << s.wnum << "LL\n#define L0DIM " << s.l0 << "LL\n";
+  // v[lane ^ M]: DPP for M = 1, 2, xor swizzle within 32 lanes up to 16, a
+  // permute through the LDS crossbar for 32.
+  o << R"(
+template <int M>
+__device__ __forceinline__ int lane_xor_bits(int v) {
+  if constexpr (M == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
+  else if constexpr (M == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
+  else if constexpr (M < 32) return __builtin_amdgcn_ds_swizzle(v, 0x1F | (M << 10));
+  else return __builtin_amdgcn_ds_bpermute((int)((threadIdx.x ^ 32u) << 2), v);
+}
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) { return __int_as_float(lane_xor_bits<M>(__float_as_int(v))); }
+template <int M>
+__device__ __forceinline__ double lane_xor(double v) {
+  return __hiloint2double(lane_xor_bits<M>(__double2hiint(v)), lane_xor_bits<M>(__double2loint(v)));
+}
+)";
+  return o.str();
+}
+
+// Components of each block a group reads, from its terms.
+struct Uses {
+  std::set<std::pair<int, int>> x, y, o;           // (block, component)
+  std::set<std::tuple<int, int, int, int>> xy;     // (xb, i, yb, j)
+};
+
+Uses uses_of(const USpec& s, const UGroup& g) {
+  Uses u;
+  for (int p : g.paths) {
+    const UPath& q = s.paths[p];
+    for (const UTerm& t : q.terms) {
+      u.x.insert({q.xb, t.i});
+      u.y.insert({q.yb, t.j});
+      u.o.insert({q.ob, t.k});
+      u.xy.insert({q.xb, t.i, q.yb, t.j});
+    }
+  }
+  return u;
+}
+
+std::string xy_name(int xb, int i, int yb, int j) {
+  return "xy" + std::to_string(xb) + "_" + std::to_string(i) + "_" + std::to_string(yb) + "_" + std::to_string(j);
+}
+
+// Emits `real name = sum_n a_n * b_n` as one multiply and a chain of FMAs.
+void fma_sum(Code& c, const std::string& name, const std::vector<std::pair<std::string, std::string>>& products) {
+  if (products.empty()) {
+    c.line("        const real %s = 0;", name.c_str());
+    return;
+  }
+  c.line("        real %s = %s * %s;", name.c_str(), products[0].first.c_str(), products[0].second.c_str());
+  for (size_t n = 1; n < products.size(); ++n)
+    c.line("        %s = FMA(%s, %s, %s);", name.c_str(), products[n].first.c_str(), products[n].second.c_str(),
+           name.c_str());
+}
+
+std::string sfx(int a, int b) { return std::to_string(a) + "_" + std::to_string(b); }
+
+// Sum of `names` over the lanes whose bit `from`..32 differ (one exchange per bit).
+void lane_sum(Code& c, const std::vector<std::string>& names, int from, int to, const char* indent) {
+  for (int m = from; m <= to; m *= 2)
+    for (const std::string& n : names) c.line("%s%s += lane_xor<%d>(%s);", indent, n.c_str(), m, n.c_str());
+}
+
+// Kernel head shared by both directions: wave -> (node, slot), lane -> (sub, u).
+void emit_head(Code& c, const char* order_name, int slots) {
+  c.line("  const i64 item = (i64)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
+  c.line("  if (item >= items) return;");
+  c.line("  const int lane = threadIdx.x & 63;");
+  c.line("  const int slot = (int)(item %% %d);", slots);
+  c.line("  const int node = %s[item / %d];", order_name, slots);
+}
+
+void emit_group_lanes(Code& c, const UGroup& g) {
+  int log = 0;
+  while ((1 << log) < g.cw) ++log;
+  c.line("    const int chunk = slot;");
+  c.line("    const int u = chunk * 64 + (lane & %d);", g.cw - 1);
+  c.line("    const int sub = lane >> %d;", log);
+  c.line("    const bool act = u < %d;", g.ch);
+}
+
+std::string emit_forward(const UuuPlan& plan, bool env, bool l0) {
+  const USpec& s = plan.spec;
+  Code c;
+  c.s << prelude(s);
+  for (size_t gi = 0; gi < plan.fwd.size(); ++gi) {
+    const UGroup& g = plan.fwd[gi];
+    const Uses use = uses_of(s, g);
+    const int nsub = 64 / g.cw;
+    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uuu_fwd_g%d(", (int)gi);
+    c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
+    c.line("    const real* __restrict__ env, const int* __restrict__ src, const int* __restrict__ rowptr,");
+    c.line("    const int* __restrict__ order, real* __restrict__ out, real* __restrict__ l0, i64 items) {");
+    emit_head(c, "order", g.chunks);
+    c.line("  const int beg = rowptr[node], end = rowptr[node + 1];");
+    c.line("  {");
+    emit_group_lanes(c, g);
+    std::vector<std::string> accs;
+    for (int b : g.obs)
+      for (int k = 0; k < s.oblocks[b].d; ++k) {
+        accs.push_back("o" + std::to_string(b) + "_" + std::to_string(k));
+        c.line("    real %s = 0;", accs.back().c_str());
+      }
+    c.line("    for (int e0 = beg; e0 < end; e0 += %d) {", nsub);
+    c.line("      const int e = e0 + sub;");
+    c.line("      if (act && e < end) {");
+    c.line("        const i64 sn = src[e];");
+    for (int b : g.xbs)
+      c.line("        const real* xr%d = x + sn * IN1 + %d + (i64)u * %d;", b, s.xblocks[b].off, s.xblocks[b].d);
+    for (int b : g.ybs)
+      c.line("        const real* yr%d = y + (i64)e * IN2 + %d + (i64)u * %d;", b, s.yblocks[b].off, s.yblocks[b].d);
+    for (const auto& xi : use.x) c.line("        const real x%d_%d = xr%d[%d];", xi.first, xi.second, xi.first, xi.second);
+    for (const auto& yj : use.y)
+      c.line("        const real y%d_%d = __builtin_nontemporal_load(yr%d + %d);", yj.first, yj.second, yj.first,
+             yj.second);
+    if (env) c.line("        const real ev = env[e];");
+    for (int p : g.paths)
+      if (s.paths[p].w_off >= 0)
+        c.line("        const real w%d = __builtin_nontemporal_load(w + (i64)e * WNUM + %d + u);", p, s.paths[p].w_off);
+    for (const auto& q : use.xy) {
+      const auto [xb, i, yb, j] = q;
+      c.line("        const real %s = x%d_%d * y%d_%d;", xy_name(xb, i, yb, j).c_str(), xb, i, yb, j);
+    }
+    for (int p : g.paths) {
+      const UPath& q = s.paths[p];
+      std::map<int, std::vector<const UTerm*>> by_k;
+      for (const UTerm& t : q.terms) by_k[t.k].push_back(&t);
+      if (by_k.empty()) continue;
+      std::string scale = q.w_off >= 0 ? "w" + std::to_string(p) : "";
+      if (env) scale = scale.empty() ? "ev" : "ev * " + scale;
+      if (!scale.empty()) c.line("        const real a%d = %s;", p, scale.c_str());
+      for (const auto& kv : by_k) {
+        std::vector<std::pair<std::string, std::string>> products;
+        for (const UTerm* t : kv.second) products.push_back({lit(t->c, s.bits), xy_name(q.xb, t->i, q.yb, t->j)});
+        fma_sum(c, "t" + sfx(p, kv.first), products);
+        if (scale.empty())
+          c.line("        o%d_%d += t%d_%d;", q.ob, kv.first, p, kv.first);
+        else
+          c.line("        o%d_%d = FMA(a%d, t%d_%d, o%d_%d);", q.ob, kv.first, p, p, kv.first, q.ob, kv.first);
+      }
+      if (l0 && q.l0_col >= 0) {
+        const bool has0 = by_k.count(0) > 0;
+        std::string v = has0 ? "t" + std::to_string(p) + "_0" : "(real)0";
+        if (q.w_off >= 0 && has0) v = "w" + std::to_string(p) + " * " + v;
+        c.line("        l0[(i64)e * L0DIM + %d + u] = %s;", q.l0_col, v.c_str());
+      }
+    }
+    c.line("      }");
+    c.line("    }");
+    if (nsub > 1) lane_sum(c, accs, g.cw, 32, "    ");
+    c.line("    if (sub == 0 && act) {");
+    c.line("      real* orow = out + (i64)node * OUTD;");
+    for (int b : g.obs)
+      for (int k = 0; k < s.oblocks[b].d; ++k)
+        c.line("      orow[%d + u * %d] = o%d_%d;", s.oblocks[b].off + k, s.oblocks[b].d, b, k);
+    c.line("    }");
+    c.line("  }");
+    c.line("}");
+  }
+  return c.s.str();
+}
+
+std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx, bool want_gy,
+                          bool want_gw, bool want_genv) {
+  const USpec& s = plan.spec;
+  Code c;
+  c.s << prelude(s);
+  for (size_t gi = 0; gi < plan.bwd.size(); ++gi) {
+    const UGroup& g = plan.bwd[gi];
+    const Uses use = uses_of(s, g);
+    const int nsub = 64 / g.cw;
+    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uuu_bwd_g%d(", (int)gi);
+    c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
+    c.line("    const real* __restrict__ env, const real* __restrict__ g, const real* __restrict__ gl0,");
+    c.line("    const int* __restrict__ dst, const int* __restrict__ rowptr, const int* __restrict__ edge_ids,");
+    c.line("    const int* __restrict__ order, real* __restrict__ gx, real* gy, real* __restrict__ gw,");
+    c.line("    real* __restrict__ part, i64 items, i64 num_edges) {");
+    emit_head(c, "order", g.chunks);
+    c.line("  const int beg = rowptr[node], end = rowptr[node + 1];");
+    c.line("  {");
+    emit_group_lanes(c, g);
+    // The source row's input blocks, once.
+    for (const auto& xi : use.x) c.line("    real x%d_%d = 0;", xi.first, xi.second);
+    c.line("    if (act) {");
+    for (const auto& xi : use.x)
+      c.line("      x%d_%d = x[(i64)node * IN1 + %d + (i64)u * %d];", xi.first, xi.second,
+             s.xblocks[xi.first].off + xi.second, s.xblocks[xi.first].d);
+    c.line("    }");
+    std::vector<std::string> gxs;
+    if (want_gx)
+      for (int b : g.xbs)
+        for (int i = 0; i < s.xblocks[b].d; ++i) {
+          gxs.push_back("gx" + std::to_string(b) + "_" + std::to_string(i));
+          c.line("    real %s = 0;", gxs.back().c_str());
+        }
+    c.line("    for (int e0 = beg; e0 < end; e0 += %d) {", nsub);
+    c.line("      const int pos = e0 + sub;");
+    c.line("      const int e = pos < end ? edge_ids[pos] : 0;");
+    if (want_genv) c.line("      real gev = 0;");
+    c.line("      if (act && pos < end) {");
+    c.line("        const i64 dn = dst[e];");
+    for (const auto& yj : use.y)
+      c.line("        const real y%d_%d = __builtin_nontemporal_load(y + (i64)e * IN2 + %d + (i64)u * %d);", yj.first,
+             yj.second, s.yblocks[yj.first].off + yj.second, s.yblocks[yj.first].d);
+    for (const auto& ok : use.o)
+      c.line("        const real g%d_%d = g[dn * OUTD + %d + (i64)u * %d];", ok.first, ok.second,
+             s.oblocks[ok.first].off + ok.second, s.oblocks[ok.first].d);
+    if (env) {
+      c.line("        const real ev = env[e];");
+      for (const auto& ok : use.o) c.line("        const real G%d_%d = ev * g%d_%d;", ok.first, ok.second, ok.first, ok.second);
+    } else {
+      for (const auto& ok : use.o) c.line("        const real G%d_%d = g%d_%d;", ok.first, ok.second, ok.first, ok.second);
+    }
+    for (int p : g.paths)
+      if (s.paths[p].w_off >= 0 && (want_gx || want_gy || want_genv))
+        c.line("        const real w%d = __builtin_nontemporal_load(w + (i64)e * WNUM + %d + u);", p, s.paths[p].w_off);
+    const bool need_xy = want_gw || want_genv;
+    if (need_xy)
+      for (const auto& q : use.xy) {
+        const auto [xb, i, yb, j] = q;
+        c.line("        const real %s = x%d_%d * y%d_%d;", xy_name(xb, i, yb, j).c_str(), xb, i, yb, j);
+      }
+    if (want_gy)
+      for (int b : g.ybs)
+        for (int j = 0; j < s.yblocks[b].d; ++j) c.line("        real gy%d_%d = 0;", b, j);
+    for (int p : g.paths) {
+      const UPath& q = s.paths[p];
+      if (q.terms.empty()) {
+        if (want_gw && q.w_off >= 0)
+          c.line("        __builtin_nontemporal_store((real)0, gw + (i64)e * WNUM + %d + u);", q.w_off);
+        continue;
+      }
+      const bool l0path = gl0 && q.l0_col >= 0;
+      // Seeds of this path: G (env * g), plus the scalar-feature seed.
+      auto seed = [&](int k) {
+        std::string name = "G" + std::to_string(q.ob) + "_" + std::to_string(k);
+        return (l0path && k == 0) ? std::string("Gl") + std::to_string(p) : name;
+      };
+      if (l0path)
+        c.line("        const real Gl%d = G%d_0 + gl0[(i64)e * L0DIM + %d + u];", p, q.ob, q.l0_col);
+      // r_ij = sum_k c_ijk seed_k
+      std::map<std::pair<int, int>, std::vector<const UTerm*>> by_ij;
+      for (const UTerm& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
+      for (const auto& kv : by_ij) {
+        std::vector<std::pair<std::string, std::string>> products;
+        for (const UTerm* t : kv.second) products.push_back({lit(t->c, s.bits), seed(t->k)});
+        fma_sum(c, "r" + std::to_string(p) + "_" + sfx(kv.first.first, kv.first.second), products);
+      }
+      auto r_name = [&](int i, int j) { return "r" + std::to_string(p) + "_" + sfx(i, j); };
+      const std::string a = q.w_off >= 0 ? "w" + std::to_string(p) : "";
+      if (want_gw && q.w_off >= 0) {
+        std::vector<std::pair<std::string, std::string>> products;
+        for (const auto& kv : by_ij)
+          products.push_back({xy_name(q.xb, kv.first.first, q.yb, kv.first.second), r_name(kv.first.first, kv.first.second)});
+        fma_sum(c, "gw" + std::to_string(p), products);
+        c.line("        __builtin_nontemporal_store(gw%d, gw + (i64)e * WNUM + %d + u);", p, q.w_off);
+      }
+      // gx_i += a * sum_j y_j r_ij and gy_j += a * sum_i x_i r_ij
+      for (int side = 0; side < 2; ++side) {
+        if ((side == 0 && !want_gx) || (side == 1 && !want_gy)) continue;
+        std::map<int, std::vector<std::pair<std::string, std::string>>> sums;
+        for (const auto& kv : by_ij) {
+          const int i = kv.first.first, j = kv.first.second;
+          if (side == 0)
+            sums[i].push_back({"y" + sfx(q.yb, j), r_name(i, j)});
+          else
+            sums[j].push_back({"x" + sfx(q.xb, i), r_name(i, j)});
+        }
+        const int blk = side == 0 ? q.xb : q.yb;
+        const char* acc = side == 0 ? "gx" : "gy";
+        for (const auto& kv : sums) {
+          const std::string tmp = std::string(side == 0 ? "sx" : "sy") + std::to_string(p) + "_" + std::to_string(kv.first);
+          fma_sum(c, tmp, kv.second);
+          if (a.empty())
+            c.line("        %s%d_%d += %s;", acc, blk, kv.first, tmp.c_str());
+          else
+            c.line("        %s%d_%d = FMA(%s, %s, %s%d_%d);", acc, blk, kv.first, a.c_str(), tmp.c_str(), acc, blk,
+                   kv.first);
+        }
+      }
+      if (want_genv) {
+        // d out / d env = a * sum_k t_k g_k with t_k = sum c x_i y_j and the raw seed g.
+        std::map<int, std::vector<std::pair<std::string, std::string>>> by_k;
+        for (const UTerm& t : q.terms) by_k[t.k].push_back({lit(t.c, s.bits), xy_name(q.xb, t.i, q.yb, t.j)});
+        std::vector<std::pair<std::string, std::string>> dots;
+        for (const auto& kv : by_k) {
+          fma_sum(c, "t" + sfx(p, kv.first), kv.second);
+          dots.push_back({"t" + sfx(p, kv.first), "g" + sfx(q.ob, kv.first)});
+        }
+        fma_sum(c, "ge" + std::to_string(p), dots);
+        if (a.empty())
+          c.line("        gev += ge%d;", p);
+        else
+          c.line("        gev = FMA(%s, ge%d, gev);", a.c_str(), p);
+      }
+    }
+    if (want_gy)
+      for (int b : g.ybs)
+        for (int j = 0; j < s.yblocks[b].d; ++j) {
+          const long off = s.yblocks[b].off + j;
+          if (g.gy_accumulate.count(b))
+            c.line("        gy[(i64)e * IN2 + %ld + (i64)u * %d] += gy%d_%d;", off, s.yblocks[b].d, b, j);
+          else
+            c.line("        gy[(i64)e * IN2 + %ld + (i64)u * %d] = gy%d_%d;", off, s.yblocks[b].d, b, j);
+        }
+    c.line("      }");
+    if (want_genv) {
+      // Sum over the channels of this sub-group's edge; its first lane writes.
+      if (g.cw > 1) lane_sum(c, {"gev"}, 1, g.cw / 2, "      ");
+      c.line("      if ((lane & %d) == 0 && pos < end) part[(i64)(%d + chunk) * num_edges + e] = gev;", g.cw - 1,
+             g.genv_slot);
+    }
+    c.line("    }");
+    if (want_gx) {
+      if (nsub > 1) lane_sum(c, gxs, g.cw, 32, "    ");
+      c.line("    if (sub == 0 && act) {");
+      c.line("      real* xrow = gx + (i64)node * IN1;");
+      for (int b : g.xbs)
+        for (int i = 0; i < s.xblocks[b].d; ++i)
+          c.line("      xrow[%d + u * %d] = gx%d_%d;", s.xblocks[b].off + i, s.xblocks[b].d, b, i);
+      c.line("    }");
+    }
+    c.line("  }");
+    c.line("}");
+  }
+  // Sum of the env-gradient partial slots.
+  c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uuu_genv_reduce(const real* __restrict__ part,");
+  c.line("    real* __restrict__ genv, i64 num_edges) {");
+  c.line("  const i64 e = (i64)blockIdx.x * 256 + threadIdx.x;");
+  c.line("  if (e >= num_edges) return;");
+  c.line("  real acc = 0;");
+  c.line("  for (int n = 0; n < %d; ++n) acc += part[(i64)n * num_edges + e];", plan.genv_slots);
+  c.line("  genv[e] = acc;");
+  c.line("}");
+  return c.s.str();
+}
+
+std::string source_for(const UuuPlan& plan, const std::string& v) {
+  // fwd<env><l0>; bwd<env><gl0><gx><gy><gw><genv>
+  auto flag = [&](size_t i) { return v.size() > i && v[i] == '1'; };
+  if (v.compare(0, 3, "fwd") == 0) return emit_forward(plan, flag(3), flag(4));
+  return emit_backward(plan, flag(3), flag(4), flag(5), flag(6), flag(7), flag(8));
+}
+
+void check_sizes(int64_t num_nodes, int64_t num_edges) {
+  if (num_nodes < 0 || num_edges < 0) fail("negative problem size");
+  if (num_nodes > 0x7fffffffLL || num_edges > 0x7fffffffLL) fail("graph exceeds int32 indexing");
+}
+
+unsigned blocks_for(int64_t items) {
+  const int64_t blocks = (items + 3) / 4;
+  if (blocks > 0x7fffffffLL) fail("uuu: launch grid exceeds 2^31 workgroups");
+  return (unsigned)blocks;
+}
+
+}  // namespace
+}  // namespace luna
+
+using namespace luna;
+
+struct LunaUuuPlan {
+  UuuPlan plan;
+};
+
+extern "C" {
+
+int luna_uuu_plan_create(const char* spec, const char* cache_dir, LunaUuuPlan** out) {
+  return guard_call([&] {
+    if (!spec || !out) fail("luna_uuu_plan_create: null argument");
+    auto holder = std::make_unique<LunaUuuPlan>();
+    UuuPlan& p = holder->plan;
+    p.spec = parse(spec);
+    p.kernels.cache_dir = cache_dir ? cache_dir : "";
+    p.kernels.tag = "uuu";
+    const USpec& s = p.spec;
+    if (!s.paths.empty()) {
+      p.fwd = forward_groups(s);
+      p.bwd = backward_groups(s, &p.bwd_phases);
+      // Launch order: by phase (a later phase adds to the gy an earlier one wrote).
+      std::stable_sort(p.bwd.begin(), p.bwd.end(), [](const UGroup& a, const UGroup& b) { return a.phase < b.phase; });
+      for (UGroup& g : p.bwd) {
+        g.genv_slot = p.genv_slots;
+        p.genv_slots += g.chunks;
+      }
+    }
+    std::vector<std::pair<long, long>> xs, ys, os, ws;
+    for (const UPath& q : s.paths) {
+      xs.push_back({q.x_off, q.x_off + (long)q.ch * q.d1});
+      ys.push_back({q.y_off, q.y_off + (long)q.ch * q.d2});
+      os.push_back({q.out_off, q.out_off + (long)q.ch * q.d3});
+      if (q.w_off >= 0) ws.push_back({q.w_off, q.w_off + q.ch});
+    }
+    p.out_zero = !covers(os, s.out);
+    p.gx_zero = !covers(xs, s.in1);
+    p.gy_zero = !covers(ys, s.in2);
+    p.gw_zero = !covers(ws, s.wnum);
+    *out = holder.release();
+  });
+}
+
+int luna_uuu_plan_destroy(LunaUuuPlan* plan) {
+  return guard_call([&] { delete plan; });
+}
+
+int luna_uuu_plan_needs_zero(const LunaUuuPlan* plan, int32_t* flags) {
+  return guard_call([&] {
+    if (!plan || !flags) fail("luna_uuu_plan_needs_zero: null argument");
+    const UuuPlan& p = plan->plan;
+    flags[0] = p.out_zero;
+    flags[1] = p.gx_zero;
+    flags[2] = p.gy_zero;
+    flags[3] = p.gw_zero;
+  });
+}
+
+int luna_uuu_plan_precompile(LunaUuuPlan* plan) {
+  return guard_call([&] {
+    if (!plan) fail("luna_uuu_plan_precompile: null plan");
+    UuuPlan& p = plan->plan;
+    if (p.spec.paths.empty()) return;
+    for (const std::string v : {"fwd00", "bwd001110"}) p.kernels.code_for(v, [&] { return source_for(p, v); });
+  });
+}
+
+int luna_uuu_conv_fwd(const LunaUuuPlan* cplan, const void* x, const void* y, const void* w, const void* env,
+                      const int32_t* src, const int32_t* dst_rowptr, const int32_t* node_order, void* out, void* l0,
+                      int64_t num_nodes, int64_t num_edges, LunaStream stream) {
+  return guard_call([&] {
+    if (!cplan) fail("luna_uuu_conv_fwd: null plan");
+    UuuPlan& p = const_cast<LunaUuuPlan*>(cplan)->plan;
+    check_sizes(num_nodes, num_edges);
+    if (num_nodes == 0 || p.spec.paths.empty()) return;
+    if (!x || !out || !dst_rowptr || !node_order) fail("luna_uuu_conv_fwd: null tensor");
+    if (num_edges > 0 && (!y || !src || (p.spec.wnum > 0 && !w))) fail("luna_uuu_conv_fwd: null edge tensor");
+    if (l0 && p.spec.l0 == 0) l0 = nullptr;
+    const std::string v = std::string("fwd") + (env ? '1' : '0') + (l0 ? '1' : '0');
+    hipModule_t module = p.kernels.module_for(v, [&] { return source_for(p, v); });
+    for (size_t gi = 0; gi < p.fwd.size(); ++gi) {
+      int64_t items = num_nodes * p.fwd[gi].chunks;
+      void* args[] = {&x, &y, &w, &env, &src, &dst_rowptr, &node_order, &out, &l0, &items};
+      launch("uuu_fwd", function_for(module, "luna_uuu_fwd_g" + std::to_string(gi)), dim3(blocks_for(items)),
+             dim3(256), (hipStream_t)stream, args);
+    }
+  });
+}
+
+int luna_uuu_conv_bwd_workspace(const LunaUuuPlan* plan, int64_t num_nodes, int64_t num_edges, size_t* bytes) {
+  return guard_call([&] {
+    if (!plan || !bytes) fail("luna_uuu_conv_bwd_workspace: null argument");
+    check_sizes(num_nodes, num_edges);
+    const UuuPlan& p = plan->plan;
+    // Partial slots of the env gradient, needed only when several wave bodies share an edge.
+    *bytes = p.genv_slots > 1 ? (size_t)p.genv_slots * (size_t)num_edges * (p.spec.bits / 8) : 0;
+  });
+}
+
+int luna_uuu_conv_bwd(const LunaUuuPlan* cplan, const void* x, const void* y, const void* w, const void* env,
+                      const void* g, const void* gl0, const int32_t* dst, const int32_t* src_rowptr,
+                      const int32_t* edge_ids_by_src, const int32_t* source_node_order, void* gx, void* gy, void* gw,
+                      void* genv, void* workspace, size_t workspace_bytes, int64_t num_nodes, int64_t num_edges,
+                      LunaStream stream) {
+  return guard_call([&] {
+    if (!cplan) fail("luna_uuu_conv_bwd: null plan");
+    UuuPlan& p = const_cast<LunaUuuPlan*>(cplan)->plan;
+    check_sizes(num_nodes, num_edges);
+    if (num_nodes == 0 || p.spec.paths.empty()) return;
+    if (!x || !g || !src_rowptr || !source_node_order) fail("luna_uuu_conv_bwd: null tensor");
+    if (num_edges > 0 && (!y || !dst || !edge_ids_by_src || (p.spec.wnum > 0 && !w)))
+      fail("luna_uuu_conv_bwd: null edge tensor");
+    if (gl0 && p.spec.l0 == 0) gl0 = nullptr;
+    if (!env) genv = nullptr;
+    int64_t E = num_edges;
+    if (E == 0) gy = gw = genv = nullptr;  // nothing per edge; gx is still written (zeros)
+    if (!gx && !gy && !gw && !genv) return;
+    void* part = nullptr;
+    if (genv) {
+      if (p.genv_slots > 1) {
+        const size_t need = (size_t)p.genv_slots * (size_t)E * (p.spec.bits / 8);
+        if (!workspace || workspace_bytes < need) fail("luna_uuu_conv_bwd: workspace too small");
+        part = workspace;
+      } else {
+        part = genv;
+      }
+    }
+    const hipStream_t s = (hipStream_t)stream;
+    const std::string flags = std::string() + (env ? '1' : '0') + (gl0 ? '1' : '0') + (gx ? '1' : '0') +
+                              (gy ? '1' : '0') + (gw ? '1' : '0') + (genv ? '1' : '0');
+    const std::string v = "bwd" + flags;
+    hipModule_t module = p.kernels.module_for(v, [&] { return source_for(p, v); });
+    for (size_t gi = 0; gi < p.bwd.size(); ++gi) {
+      int64_t items = num_nodes * p.bwd[gi].chunks;
+      void* args[] = {&x, &y, &w, &env, &g, &gl0, &dst, &src_rowptr, &edge_ids_by_src, &source_node_order,
+                      &gx, &gy, &gw, &part, &items, &E};
+      launch("uuu_bwd", function_for(module, "luna_uuu_bwd_g" + std::to_string(gi)), dim3(blocks_for(items)),
+             dim3(256), s, args);
+    }
+    if (genv && p.genv_slots > 1) {
+      void* args[] = {&part, &genv, &E};
+      launch("uuu_genv_reduce", function_for(module, "luna_uuu_genv_reduce"), dim3((unsigned)((E + 255) / 256)),
+             dim3(256), s, args);
+    }
+  });
+}
+
+}  // extern "C"

@@ -1,9 +1,10 @@
 """Functional API: preparation and calls with explicit weights.
 
 Mirrors ``prepare_tensor_product`` / ``tensor_product_conv``
-(``src/lunatp/interface.py:147-262``) for the UVU convolution path.  Other
-connection modes of the reference (uuu, uvw convolutions, non-convolution
-products) are outside this library's scope and raise ``NotImplementedError``.
+(``src/lunatp/interface.py:147-262``) for the UVU and UUU convolutions and the
+shared-weight UVW product.  Other connection modes of the reference (uvw
+convolution, non-convolution uuu/uvu products) are outside this library's
+scope and raise ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -16,12 +17,13 @@ import torch
 
 from .irreps import Irreps
 from .layout import TensorProductPaths
+from .uuu_conv import LunaTPUUUConv, create_uuu_conv_operator
 from .uvu_conv import LunaTPUVUConv, create_uvu_conv_operator
 
 
 def _unsupported(mode: str, convolution: bool):
     kind = "convolution" if convolution else "tensor product"
-    raise NotImplementedError(f"{mode} {kind} is not part of this MI355X build (uvu convolution only)")
+    raise NotImplementedError(f"{mode} {kind} is not part of this MI355X build")
 
 
 def prepare_tensor_product(irreps_in1, irreps_in2=None, irreps_out=None, instructions=None, *,
@@ -32,9 +34,8 @@ def prepare_tensor_product(irreps_in1, irreps_in2=None, irreps_out=None, instruc
     if isinstance(irreps_in1, Mapping):
         if not convolution or mode not in ("uuu", "uvu"):
             raise ValueError('Metadata requires convolution=True and mode="uuu" or "uvu"')
-        if mode != "uvu":
-            _unsupported(mode, True)
-        return create_uvu_conv_operator(irreps_in1, dtype=dtype)
+        factory = create_uuu_conv_operator if mode == "uuu" else create_uvu_conv_operator
+        return factory(irreps_in1, dtype=dtype)
     if isinstance(irreps_in1, TensorProductPaths):
         paths = copy(irreps_in1)
     else:
@@ -58,6 +59,8 @@ def prepare_tensor_product(irreps_in1, irreps_in2=None, irreps_out=None, instruc
             from .uvw import LunaTPUVW
             return LunaTPUVW(paths, dtype=dtype)
         _unsupported(inferred, False)
+    if inferred == "uuu":
+        return create_uuu_conv_operator(paths, dtype=dtype)
     if inferred != "uvu":
         _unsupported(inferred, True)
     return create_uvu_conv_operator(paths, dtype=dtype)
@@ -114,4 +117,4 @@ def tensor_product_conv(x, edge_attr, weight=None, *, graph, irreps_in1=None, ir
 
 
 __all__ = ["prepare_tensor_product", "tensor_product", "tensor_product_conv",
-           "create_uvu_conv_operator", "LunaTPUVUConv"]
+           "create_uvu_conv_operator", "LunaTPUVUConv", "create_uuu_conv_operator", "LunaTPUUUConv"]

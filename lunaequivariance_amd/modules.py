@@ -9,6 +9,7 @@ import torch
 from .graph import make_graph
 from .interface import tensor_product_conv
 from .layout import TensorProductConfig
+from .uuu_conv import create_uuu_conv_operator
 from .uvu_conv import create_uvu_conv_operator
 
 
@@ -72,7 +73,8 @@ class TensorProductConv(torch.nn.Module):
     """Fused tensor product on every edge, summed at destination nodes.
 
     Pass irreps and instructions, an existing configuration (or e3nn-like
-    module with the same attributes), or prebuilt metadata with ``mode="uvu"``.
+    module with the same attributes), or prebuilt metadata with ``mode="uvu"`` or
+    ``mode="uuu"``.
     Build topology with ``create_graph`` and pass ``graph=`` on every call.
     """
 
@@ -115,10 +117,11 @@ class TensorProductConv(torch.nn.Module):
             weight = getattr(tp, "weight", None)
             if dtype is None:
                 dtype = weight.dtype if isinstance(weight, torch.Tensor) else torch.get_default_dtype()
-        if mode != "uvu":
+        if mode not in ("uvu", "uuu"):
             raise NotImplementedError(f"{mode} convolution is not part of this MI355X build")
         self.mode = mode + "_conv"
-        self.op = create_uvu_conv_operator(tp, dtype=dtype)
+        self._factory = create_uuu_conv_operator if mode == "uuu" else create_uvu_conv_operator
+        self.op = self._factory(tp, dtype=dtype)
         if metadata:
             self.weight_numel = tp["weight_numel"]
             self.internal_weights = self.shared_weights = False
@@ -133,8 +136,7 @@ class TensorProductConv(torch.nn.Module):
         dtype = fn(torch.empty(0, dtype=self.op.compute_dtype)).dtype
         result = super()._apply(fn, recurse=recurse)
         if dtype in (torch.float32, torch.float64) and dtype != self.op.compute_dtype:
-            self.op = create_uvu_conv_operator(self.op.meta if not hasattr(self, "tp") else self.tp,
-                                               dtype=dtype)
+            self.op = self._factory(self.op.meta if not hasattr(self, "tp") else self.tp, dtype=dtype)
         return result
 
     @staticmethod

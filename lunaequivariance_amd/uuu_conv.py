@@ -1,0 +1,326 @@
+"""UUU (channel-wise) tensor-product convolution: lowering, operator, launches.
+
+Lowering follows ``build_uuu_metadata`` (``src/lunatp/uuu/kernels/utils.py:250-330``)
+as used by ``build_uuu_conv_metadata``
+(``src/lunatp/uuu_conv/kernels/utils.py:342-364``): every uuu instruction is
+one path with ``channels = mul_in1 = mul_in2 = mul_out``, offsets into x, y
+and out, a weight offset that advances by ``channels`` over weighted
+instructions only, and sparse coefficient terms ``(i, j, k, cg * path_weight)``.
+
+The per-path message is ``a_u * sum c_ijk x[src, u, i] y[e, u, j]`` with
+``a_u = w[e, weight_offset + u]`` (1 for unweighted paths), summed at
+destinations after the optional ``env`` multiply; ``return_l0_feat`` returns
+each scalar-output path's message before ``env`` (one column per channel).
+
+Autograd reuses the convolution classes of ``uvu_conv``: they depend only on
+the operator's ``launch_forward`` / ``launch_backward`` and on
+multilinearity, so second and third derivatives run on the same two kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections import Counter
+from collections.abc import Mapping
+
+import torch
+
+from . import _native
+from .cg import sparse_terms
+from .graph import LunaTPGraph
+from .layout import TensorProductPaths
+from .uvu_conv import UVUConvForward, _check_device, _stream, l0_feature_layout
+
+
+def build_uuu_conv_metadata(tp, coefficient_dtype=torch.float32) -> dict:
+    """Path specs of a UUU configuration (``uuu/kernels/utils.py:250-330``)."""
+    if coefficient_dtype not in (torch.float32, torch.float64):
+        raise ValueError(
+            f"UUU convolution coefficients require float32 or float64; got {coefficient_dtype}.")
+    if tp.internal_weights and not tp.shared_weights:
+        raise ValueError("Internal UUU weights must be shared across items.")
+    in_slices = tp.irreps_in1.slices()
+    edge_slices = tp.irreps_in2.slices()
+    out_slices = tp.irreps_out.slices()
+    output_uses = Counter(ins.i_out for ins in tp.instructions)
+    specs = []
+    weight_offset = 0
+    max_channels = 0
+    for ins in tp.instructions:
+        if ins.connection_mode != "uuu":
+            raise ValueError(f"Only connection_mode='uuu' is supported, got {ins.connection_mode!r}.")
+        mul_in, ir_in = tp.irreps_in1[ins.i_in1]
+        mul_edge, ir_edge = tp.irreps_in2[ins.i_in2]
+        mul_out, ir_out = tp.irreps_out[ins.i_out]
+        channels = int(mul_in)
+        if channels != int(mul_edge) or channels != int(mul_out):
+            raise ValueError("UUU generated kernels require mul_in1 == mul_in2 == mul_out for every path.")
+        if tuple(int(v) for v in ins.path_shape) != (channels,):
+            raise ValueError("UUU generated kernels expect uuu path_shape=(channels,).")
+        if channels == 0:
+            continue
+        max_channels = max(max_channels, channels)
+        path_weight = float(ins.path_weight)
+        terms = [] if path_weight == 0 else sparse_terms(ir_in.l, ir_edge.l, ir_out.l, path_weight)
+        if coefficient_dtype == torch.float32:
+            terms = [(i, j, k, float(torch.tensor(c, dtype=torch.float32))) for i, j, k, c in terms]
+        specs.append({
+            "x_offset": in_slices[ins.i_in1].start,
+            "y_offset": edge_slices[ins.i_in2].start,
+            "out_offset": out_slices[ins.i_out].start,
+            "accumulate_output": output_uses[ins.i_out] > 1,
+            "weight_offset": weight_offset,
+            "has_weight": bool(ins.has_weight),
+            "path_weight": path_weight,
+            "channels": channels,
+            "d1": ir_in.dim, "d2": ir_edge.dim, "d3": ir_out.dim,
+            "l1": ir_in.l, "l2": ir_edge.l, "l3": ir_out.l,
+            "terms": terms,
+        })
+        if ins.has_weight:
+            weight_offset += channels
+    if weight_offset != tp.weight_numel:
+        raise ValueError(
+            f"lowered weight_numel={weight_offset}, configuration reports {tp.weight_numel}.")
+    return {
+        "in1_dim": tp.irreps_in1.dim,
+        "in2_dim": tp.irreps_in2.dim,
+        "out_dim": tp.irreps_out.dim,
+        "weight_numel": tp.weight_numel,
+        "max_channels": max_channels,
+        "generated_specs": specs,
+    }
+
+
+def spec_text(meta: dict, dtype: torch.dtype) -> str:
+    """Serialise path specs into the C-ABI's UUU plan specification.
+
+    With ``meta["weight_linear"]`` only the weighted paths are emitted (l0
+    columns keep the positions of the full configuration).
+    """
+    specs = meta["generated_specs"]
+    offsets, l0_dim = l0_feature_layout(specs)
+    keep = [n for n, spec in enumerate(specs) if _kept(meta, spec)]
+    bits = 64 if dtype == torch.float64 else 32
+    parts = [f"LUNAUUU1 {bits} {meta['in1_dim']} {meta['in2_dim']} {meta['out_dim']} "
+             f"{meta['weight_numel']} {len(keep)} {l0_dim}"]
+    for index in keep:
+        spec = specs[index]
+        terms = spec["terms"]
+        w_off = int(spec["weight_offset"]) if spec.get("has_weight", True) else -1
+        head = (f"{spec['x_offset']} {spec['y_offset']} {spec['out_offset']} {w_off} {spec['channels']} "
+                f"{spec['d1']} {spec['d2']} {spec['d3']} {offsets.get(index, -1)} {len(terms)}")
+        body = " ".join(f"{int(i)} {int(j)} {int(k)} {float(c)!r}" for i, j, k, c in terms)
+        parts.append(head + (" " + body if body else ""))
+    return "\n".join(parts) + "\n"
+
+
+def _kept(meta, spec) -> bool:
+    return not meta.get("weight_linear") or spec.get("has_weight", True)
+
+
+class NativeUuuPlan:
+    """Owner of one C-ABI UUU plan handle."""
+
+    def __init__(self, text: str):
+        lib = _native.lib()
+        handle = ctypes.c_void_p()
+        _native.check(lib.luna_uuu_plan_create(text.encode(), _native.cache_dir().encode(),
+                                               ctypes.byref(handle)), "luna_uuu_plan_create")
+        self.handle = handle
+        flags = (ctypes.c_int32 * 4)()
+        _native.check(lib.luna_uuu_plan_needs_zero(handle, flags), "luna_uuu_plan_needs_zero")
+        self.out_zero, self.gx_zero, self.gy_zero, self.gw_zero = (bool(f) for f in flags)
+
+    def precompile(self):
+        _native.check(_native.lib().luna_uuu_plan_precompile(self.handle), "luna_uuu_plan_precompile")
+
+    def __del__(self):
+        handle = getattr(self, "handle", None)
+        try:
+            if handle is not None and _native._lib is not None:
+                _native._lib.luna_uuu_plan_destroy(handle)
+        except Exception:  # interpreter shutdown
+            pass
+        self.handle = None
+
+
+class LunaTPUUUConv:
+    """Prepared UUU convolution (``src/lunatp/interface.py:338-350``)."""
+
+    mode = "uuu_conv"
+    index_mode = "uuu_conv"
+
+    def __init__(self, meta, *, dtype=torch.float32, index_bits=32):
+        if dtype not in (torch.float32, torch.float64):
+            raise ValueError("UUU convolution requires float32 or float64.")
+        if index_bits != 32:
+            raise ValueError("only 32-bit graph indexing is supported")
+        specs = list(meta["generated_specs"])
+        if any(int(s["channels"]) < 0 for s in specs):
+            raise ValueError("UUU convolution requires nonnegative channels for every path.")
+        specs = [s for s in specs if int(s["channels"]) > 0]
+        self.meta = dict(meta, generated_specs=specs)
+        self.compute_dtype = dtype
+        self.index_bits = index_bits
+        self.in1_dim = int(meta["in1_dim"])
+        self.in2_dim = int(meta["in2_dim"])
+        self.out_dim = int(meta["out_dim"])
+        self.weight_numel = int(meta["weight_numel"])
+        self.max_channels = int(meta["max_channels"])
+        self.generated_specs = specs
+        self.l0_offsets, self.l0_dim = l0_feature_layout(specs)
+        # Paths in the kernels: all, or the weighted ones for the weight-linear part.
+        self.active_specs = [spec for spec in specs if _kept(self.meta, spec)]
+        self.l0_complete = all(_kept(self.meta, specs[n]) for n in self.l0_offsets)
+        self.spec = spec_text(self.meta, dtype)
+        self._plan = None
+        self._weight_linear = None
+        from .ops import operator_config
+
+        self.torch_config = operator_config(self)
+
+    @property
+    def plan(self) -> NativeUuuPlan:
+        if self._plan is None:
+            self._plan = NativeUuuPlan(self.spec)
+        return self._plan
+
+    def weight_linear(self):
+        """The operator restricted to weighted paths.
+
+        Unweighted paths make the convolution affine, not linear, in the
+        weights: the derivative along a weight direction ``rw`` is the
+        weighted paths evaluated at ``rw``, which this operator computes.
+        """
+        if all(spec.get("has_weight", True) for spec in self.generated_specs):
+            return self
+        if self._weight_linear is None:
+            self._weight_linear = LunaTPUUUConv(dict(self.meta, weight_linear=True), dtype=self.compute_dtype)
+        return self._weight_linear
+
+    def run(self, x, edge_attr, weight=None, *, graph, env=None, return_l0_feat=False):
+        return lunatp_uuu_conv_func(self, x, edge_attr, weight, graph=graph, env=env,
+                                    return_l0_feat=return_l0_feat)
+
+    def launch_forward(self, x, y, w, graph, env=None, want_l0=False):
+        return run_forward(self, x, y, w, graph, env, want_l0)
+
+    def launch_backward(self, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, True, True)):
+        return run_backward(self, x, y, w, graph, g, env, gl0, needs)
+
+    def __getstate__(self):
+        state = dict(self.__dict__)
+        state["_plan"] = None
+        state["_weight_linear"] = None
+        return state
+
+
+def create_uuu_conv_operator(tp_or_meta, *, dtype=None):
+    """Prepared operator from a configuration or prebuilt metadata (``lunatp/interface.py:96-120``)."""
+    if not isinstance(tp_or_meta, Mapping):
+        tp_or_meta = TensorProductPaths.from_tensor_product(tp_or_meta)
+    if dtype is None:
+        dtype = torch.float32
+    elif dtype is not torch.float32 and dtype is not torch.float64:
+        raise ValueError("UUU convolution requires float32 or float64.")
+    meta = tp_or_meta if isinstance(tp_or_meta, Mapping) else build_uuu_conv_metadata(tp_or_meta, dtype)
+    return LunaTPUUUConv(meta, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# Kernel calls (no autograd)
+# ---------------------------------------------------------------------------
+
+def _new(op, shape, zero, like):
+    return (torch.zeros if zero else torch.empty)(shape, device=like.device, dtype=like.dtype)
+
+
+def run_forward(op, x, y, w, graph, env=None, want_l0=False):
+    """out [N, out_dim] (and l0 [E, l0_dim]) from the forward kernel."""
+    _check_device(op, graph, x, y, w, env)
+    N, E = graph.num_nodes, graph.num_edges
+    if x.shape != (N, op.in1_dim):
+        raise ValueError(f"x must have shape ({N}, {op.in1_dim}); got {tuple(x.shape)}")
+    if y.shape != (E, op.in2_dim) or w.shape != (E, op.weight_numel):
+        raise ValueError("edge_attr/weight rows must match the graph's edges")
+    plan = op.plan
+    active = bool(op.active_specs)
+    out = _new(op, (N, op.out_dim), plan.out_zero or not active, x)
+    # Every edge lies in one destination row, so the kernel writes every l0 entry.
+    l0 = _new(op, (E, op.l0_dim), not (N and active and op.l0_complete), x) if want_l0 else None
+    if N and active:
+        _native.check(_native.lib().luna_uuu_conv_fwd(
+            plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w) if w.numel() else None,
+            _native.ptr(env), graph.src.data_ptr(), graph.dst_rowptr.data_ptr(), graph.node_order.data_ptr(),
+            out.data_ptr(), _native.ptr(l0) if (l0 is not None and l0.numel()) else None,
+            N, E, _stream(x)), "luna_uuu_conv_fwd")
+    return out, l0
+
+
+def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, True, True)):
+    """(gx, gy, gw, genv) from the source-owned backward kernel."""
+    _check_device(op, graph, x, y, w, env, g, gl0)
+    N, E = graph.num_nodes, graph.num_edges
+    plan = op.plan
+    need_x, need_y, need_w, need_env = needs
+    need_env = need_env and env is not None
+    active = bool(op.active_specs)
+    empty = not active or not E
+    gx = _new(op, (N, op.in1_dim), plan.gx_zero or not active, x) if need_x else None
+    gy = _new(op, (E, op.in2_dim), plan.gy_zero or empty, x) if need_y else None
+    gw = _new(op, (E, op.weight_numel), plan.gw_zero or empty, x) if need_w else None
+    genv = _new(op, (E,), empty, x) if need_env else None
+    if N and active and (need_x or ((need_y or need_w or need_env) and E)):
+        lib = _native.lib()
+        size = ctypes.c_size_t()
+        _native.check(lib.luna_uuu_conv_bwd_workspace(plan.handle, N, E, ctypes.byref(size)),
+                      "luna_uuu_conv_bwd_workspace")
+        workspace = None
+        if need_env and size.value:
+            workspace = torch.empty(size.value, device=x.device, dtype=torch.uint8)
+        _native.check(lib.luna_uuu_conv_bwd(
+            plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w) if w.numel() else None, _native.ptr(env),
+            g.data_ptr(), _native.ptr(gl0) if (gl0 is not None and gl0.numel()) else None,
+            graph.dst.data_ptr(), graph.src_rowptr.data_ptr(), graph.edge_ids_by_src.data_ptr(),
+            graph.source_node_order.data_ptr(),
+            _native.ptr(gx), _native.ptr(gy), _native.ptr(gw) if (gw is not None and gw.numel()) else None,
+            _native.ptr(genv), _native.ptr(workspace), size.value if workspace is not None else 0,
+            N, E, _stream(x)), "luna_uuu_conv_bwd")
+    return gx, gy, gw, genv
+
+
+def lunatp_uuu_conv_func(op, x, edge_attr, weight=None, *, graph: LunaTPGraph, env=None,
+                         return_l0_feat=False):
+    """Aggregate UUU edge messages at destination nodes (``uuu_conv/interface.py:153-238``).
+
+    x [num_nodes, in1_dim], edge_attr [num_edges, in2_dim]; weight is per-edge
+    [num_edges, weight_numel], shared [weight_numel] or [1, weight_numel]
+    (expanded to every edge), or None when the configuration has no weights.
+    env [num_edges] or [num_edges, 1].  Returns out [num_nodes, out_dim], or
+    (out, l0_feat [num_edges, l0_dim]).
+    """
+    num_edges = edge_attr.shape[0]
+    if weight is None:
+        if op.weight_numel != 0:
+            raise ValueError("UUU convolution with weighted paths requires weights")
+        weight = x.new_empty((num_edges, 0))
+    if weight.shape in ((op.weight_numel,), (1, op.weight_numel)):
+        weight = weight.reshape(1, -1).expand(num_edges, -1)
+    x = x.contiguous()
+    edge_attr = edge_attr.contiguous()
+    weight = weight.contiguous()
+    if env is not None:
+        env = env.reshape(-1).contiguous()
+    if torch.compiler.is_compiling():
+        from . import ops
+
+        out, l0 = torch.ops.lunaeq_amd.uuu_conv_forward(
+            x, edge_attr, weight, env, ops.graph_tables(graph), graph.num_nodes, bool(return_l0_feat),
+            op.torch_config)
+        return (out, l0) if return_l0_feat else out
+    return UVUConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
+
+
+__all__ = ["build_uuu_conv_metadata", "spec_text", "LunaTPUUUConv", "create_uuu_conv_operator",
+           "lunatp_uuu_conv_func", "run_forward", "run_backward", "NativeUuuPlan"]

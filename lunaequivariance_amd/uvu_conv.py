@@ -194,6 +194,16 @@ class LunaTPUVUConv:
         return lunatp_uvu_conv_func(self, x, edge_attr, weight, graph=graph, env=env,
                                     return_l0_feat=return_l0_feat)
 
+    def weight_linear(self):
+        """Every uvu path is weighted: the convolution is linear in the weights."""
+        return self
+
+    def launch_forward(self, x, y, w, graph, env=None, want_l0=False):
+        return run_forward(self, x, y, w, graph, env, want_l0)
+
+    def launch_backward(self, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, True, True)):
+        return run_backward(self, x, y, w, graph, g, env, gl0, needs)
+
     def __getstate__(self):
         state = dict(self.__dict__)
         state["_plan"] = None
@@ -229,7 +239,7 @@ def _check_device(op, graph, *tensors):
         if t is None:
             continue
         if not t.is_cuda:
-            raise RuntimeError("UVU convolution kernels run on the GPU; got a CPU tensor")
+            raise RuntimeError("convolution kernels run on the GPU; got a CPU tensor")
         if t.dtype != op.compute_dtype:
             raise TypeError(f"expected {op.compute_dtype}, got {t.dtype}")
     if not graph.src.is_cuda:
@@ -298,6 +308,10 @@ def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, T
 
 # ---------------------------------------------------------------------------
 # Autograd
+#
+# Shared by every convolution operator: the classes call the operator's
+# ``launch_forward`` / ``launch_backward`` kernels, and the higher-order rules
+# only use multilinearity, which holds for the uvu and uuu connections alike.
 # ---------------------------------------------------------------------------
 
 def _contig(t):
@@ -320,7 +334,7 @@ class UVUConvForward(torch.autograd.Function):
         ctx.op, ctx.graph, ctx.want_l0 = op, graph, want_l0
         ctx.save_for_backward(x, y, w, env)
         ctx.set_materialize_grads(False)
-        out, l0 = run_forward(op, x, y, w, graph, env, want_l0)
+        out, l0 = op.launch_forward(x, y, w, graph, env, want_l0)
         if want_l0:
             return out, l0
         return out
@@ -352,7 +366,7 @@ class UVUConvBackward(torch.autograd.Function):
         ctx.op, ctx.graph = op, graph
         ctx.save_for_backward(x, y, w, env, g, gl0)
         ctx.set_materialize_grads(False)
-        return run_backward(op, x, y, w, graph, g, env, gl0, needs)
+        return op.launch_backward(x, y, w, graph, g, env, gl0, needs)
 
     @staticmethod
     def backward(ctx, rx, ry, rw, renv):
@@ -370,11 +384,13 @@ class UVUConvBackward(torch.autograd.Function):
                 continue
             substituted = list(args)
             substituted[slot] = direction
+            # Along a weight direction only the weighted paths vary.
+            sop = op.weight_linear() if slot == 2 else op
             # The scalar features do not depend on env: an env direction moves
             # only the node output, and the gl0 seed drops out of its terms.
             scalar = want_l0 and slot != 3
             if need[7] or (need[8] and scalar):
-                result = conv_forward(op, graph, scalar, *substituted)
+                result = conv_forward(sop, graph, scalar, *substituted)
                 if scalar:
                     out, l0 = result
                     hl0 = _add(hl0, l0)
@@ -384,7 +400,7 @@ class UVUConvBackward(torch.autograd.Function):
             wanted = tuple(need[3 + other] and other != slot and args[other] is not None
                            for other in range(4))
             if any(wanted):
-                parts = conv_backward(op, graph, *substituted, g, gl0 if slot != 3 else None,
+                parts = conv_backward(sop, graph, *substituted, g, gl0 if slot != 3 else None,
                                       needs=wanted)
                 for other in range(4):
                     if wanted[other] and parts[other] is not None:
@@ -397,7 +413,7 @@ def conv_backward(op, graph, x, y, w, env, g, gl0, needs=(True, True, True, True
     needs = tuple(bool(n) for n in needs)
     if torch.is_grad_enabled():
         return UVUConvBackward.apply(op, graph, needs, x, y, w, env, g, gl0)
-    return run_backward(op, x, y, w, graph, g, env, gl0, needs)
+    return op.launch_backward(x, y, w, graph, g, env, gl0, needs)
 
 
 def lunatp_uvu_conv_func(op, x, edge_attr, weight, *, graph: LunaTPGraph, env=None,

@@ -1,4 +1,4 @@
-"""Dense fp64 restatement of the reference's oracle for the UVU convolution.
+"""Dense fp64 restatement of the reference's oracle for the UVU and UUU convolutions.
 
 The reference checks its kernels against e3nn's ``o3.TensorProduct`` applied
 to ``x[src]`` followed by ``index_add`` over ``dst``
@@ -12,7 +12,17 @@ multiplicity ``m2``:
                                           y[e, i2][v, j] w[e, off + u*m2 + v]
     out[n] = sum_{e: dst_e = n} env_e * msg[e]
 
-and the scalar-path features (``src/utils/testing.py:55-70``) are the per-edge
+For a uuu instruction (``docs/operators/tensor_product.md:100-106``; the
+reference's UUU conv tests use the same e3nn-then-``index_add`` oracle,
+``tests/lunatp/test_uuu_conv.py:30-45``) the channels are matched instead of
+mixed, and unweighted paths use weight 1:
+
+    msg[e, io][u, k] = pw * sum_{i, j} C[i, j, k] x[src_e, i1][u, i] y[e, i2][u, j]
+                       * (w[e, off + u] if has_weight else 1)
+
+with ``off`` advancing by ``mul`` over weighted uuu instructions only.
+
+The scalar-path features (``src/utils/testing.py:55-70``) are the per-edge
 ``msg`` columns of instructions whose output has l = 0, before ``env``,
 concatenated in output order.  Everything is differentiable torch fp64 code,
 so gradients of any order come from autograd.
@@ -79,9 +89,7 @@ def edge_messages(in1, in2, out, instructions, x_src, y, w, weights=None):
     pieces = []
     w_off = 0
     msg = x_src.new_zeros((E, out_dim))
-    for (i1, i2, io, mode, _has_w, *_), pw in zip(instructions, weights):
-        if mode != "uvu":
-            raise ValueError("oracle covers uvu instructions")
+    for (i1, i2, io, mode, has_w, *_), pw in zip(instructions, weights):
         m1, l1, _ = in1[i1]
         m2, l2, _ = in2[i2]
         mo, l3, _ = out[io]
@@ -89,17 +97,27 @@ def edge_messages(in1, in2, out, instructions, x_src, y, w, weights=None):
         cg = torch.tensor(wigner_3j(l1, l2, l3), dtype=x_src.dtype)
         xb = x_src[:, x_off[i1]: x_off[i1] + m1 * d1].reshape(E, m1, d1)
         yb = y[:, y_off[i2]: y_off[i2] + m2 * d2].reshape(E, m2, d2)
-        wb = w[:, w_off: w_off + m1 * m2].reshape(E, m1, m2)
-        piece = pw * torch.einsum("ijk,eui,evj,euv->euk", cg, xb, yb, wb).reshape(E, mo * d3)
+        if mode == "uvu":
+            wb = w[:, w_off: w_off + m1 * m2].reshape(E, m1, m2)
+            piece = pw * torch.einsum("ijk,eui,evj,euv->euk", cg, xb, yb, wb).reshape(E, mo * d3)
+            w_off += m1 * m2
+        elif mode == "uuu":
+            if not m1 == m2 == mo:
+                raise ValueError("uuu instructions need equal multiplicities")
+            wb = w[:, w_off: w_off + m1] if has_w else xb.new_ones((E, m1))
+            piece = pw * torch.einsum("ijk,eui,euj,eu->euk", cg, xb, yb, wb).reshape(E, mo * d3)
+            w_off += m1 if has_w else 0
+        else:
+            raise ValueError("oracle covers uvu and uuu instructions")
         pieces.append((io, piece))
         msg = msg + torch.nn.functional.pad(piece, (o_off[io], out_dim - o_off[io] - mo * d3))
-        w_off += m1 * m2
     return msg, pieces
 
 
-def uvu_conv(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, dst, num_nodes,
+def conv(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, dst, num_nodes,
              env=None, return_l0=False):
-    """Reference semantics of ``TensorProductConv(...)(x, y, w, graph=..., env=, return_l0_feat=)``."""
+    """Reference semantics of ``TensorProductConv(...)(x, y, w, graph=..., env=, return_l0_feat=)``
+    for uvu or uuu instructions."""
     in1, in2, out = parse_irreps(irreps_in1), parse_irreps(irreps_in2), parse_irreps(irreps_out)
     src = torch.as_tensor(src).long()
     dst = torch.as_tensor(dst).long()
@@ -124,21 +142,29 @@ def brute_force(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, 
     result = np.zeros((num_nodes, out_dim))
     for e in range(len(src)):
         w_off = 0
-        for (i1, i2, io, _m, _h, *_), pw in zip(instructions, weights):
+        for (i1, i2, io, mode, has_w, *_), pw in zip(instructions, weights):
             m1, l1, _ = in1[i1]
             m2, l2, _ = in2[i2]
             _, l3, _ = out[io]
             cg = wigner_3j(l1, l2, l3)
-            for u in range(m1):
-                for v in range(m2):
-                    for i in range(2 * l1 + 1):
-                        for j in range(2 * l2 + 1):
-                            for k in range(2 * l3 + 1):
-                                c = cg[i, j, k]
-                                if c == 0.0:
-                                    continue
-                                result[dst[e], o_off[io] + u * (2 * l3 + 1) + k] += (
-                                    pw * c * x[src[e], x_off[i1] + u * (2 * l1 + 1) + i]
-                                    * y[e, y_off[i2] + v * (2 * l2 + 1) + j] * w[e, w_off + u * m2 + v])
-            w_off += m1 * m2
+            # uvu: every (u, v) pair; uuu: the matched pairs (u, u) only.
+            pairs = [(u, v) for u in range(m1) for v in range(m2)] if mode == "uvu" else [(u, u) for u in range(m1)]
+            for u, v in pairs:
+                if mode == "uvu":
+                    weight = w[e, w_off + u * m2 + v]
+                else:
+                    weight = w[e, w_off + u] if has_w else 1.0
+                for i in range(2 * l1 + 1):
+                    for j in range(2 * l2 + 1):
+                        for k in range(2 * l3 + 1):
+                            c = cg[i, j, k]
+                            if c == 0.0:
+                                continue
+                            result[dst[e], o_off[io] + u * (2 * l3 + 1) + k] += (
+                                pw * c * x[src[e], x_off[i1] + u * (2 * l1 + 1) + i]
+                                * y[e, y_off[i2] + v * (2 * l2 + 1) + j] * weight)
+            w_off += m1 * m2 if mode == "uvu" else (m1 if has_w else 0)
     return result
+
+
+uvu_conv = conv  # the name the uvu tests and fixtures use

@@ -1,0 +1,257 @@
+"""UUU convolution on the CPU: the oracle against fixed facts, the lowering and the C-ABI plan.
+
+The oracle's uuu branch is pinned by
+  * a scalar-loop brute force (channels matched, unweighted paths weight 1);
+  * closed forms: 0e x 0e -> 0e is the product w x y; 1o x 1o -> 0e is the dot
+    product / sqrt(3) (the docs example, docs/operators/tensor_product.md:108-130);
+  * a cross-mode identity: a uuu product whose edge features repeat the same
+    vector on every channel equals the (separately pinned) uvu product with one
+    edge channel, since both normalise with fan 1 and index weights by u;
+  * rotation equivariance and fp64 gradcheck / gradgradcheck.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.uvu_conv import brute_force, conv, parse_irreps
+from tests.test_oracle_conv import block_diag_d, rotation
+
+
+def uuu_paths(in1, in2, out, unweighted=()):
+    from lunaequivariance_amd import Irreps
+
+    a, b, c = Irreps(in1), Irreps(in2), Irreps(out)
+    paths = [(i, j, k, "uuu", True) for i, (m, x) in enumerate(a) for j, (n, y) in enumerate(b)
+             for k, (o, z) in enumerate(c) if z in x * y and m == n == o]
+    return [p[:4] + (False,) if n in unweighted else p for n, p in enumerate(paths)]
+
+
+def dims(*texts):
+    return [sum(m * (2 * l + 1) for m, l, _ in parse_irreps(t)) for t in texts]
+
+
+def weight_numel(in1, instructions):
+    a = parse_irreps(in1)
+    return sum(a[i][0] for i, _, _, _, has_w, *_ in instructions if has_w)
+
+
+def problem(in1, in2, out, instructions, nodes, edges, seed):
+    gen = torch.Generator().manual_seed(seed)
+    d1, d2, _ = dims(in1, in2, out)
+    x = torch.randn(nodes, d1, generator=gen, dtype=torch.float64)
+    y = torch.randn(edges, d2, generator=gen, dtype=torch.float64)
+    w = torch.randn(edges, weight_numel(in1, instructions), generator=gen, dtype=torch.float64)
+    src = torch.randint(nodes, (edges,), generator=gen)
+    dst = torch.sort(torch.randint(nodes, (edges,), generator=gen))[0]
+    return x, y, w, src, dst
+
+
+def test_oracle_matches_brute_force():
+    in1, in2, out = "3x0e+3x1o+2x2e", "3x1o+3x0e+2x2e", "3x0e+3x1o+2x2e+2x1e"
+    instructions = uuu_paths(in1, in2, out, unweighted=(1, 4))
+    x, y, w, src, dst = problem(in1, in2, out, instructions, 5, 11, 0)
+    dense = conv(in1, in2, out, instructions, x, y, w, src, dst, 5)
+    loops = brute_force(in1, in2, out, instructions, x, y, w, src.numpy(), dst.numpy(), 5)
+    assert np.allclose(dense.numpy(), loops, atol=1e-12)
+
+
+def test_scalar_product_closed_form():
+    x, y, w, src, dst = problem("6x0e", "6x0e", "6x0e", [(0, 0, 0, "uuu", True)], 4, 9, 1)
+    out = conv("6x0e", "6x0e", "6x0e", [(0, 0, 0, "uuu", True)], x, y, w, src, dst, 4)
+    expected = torch.zeros(4, 6, dtype=torch.float64).index_add(0, dst, x[src] * y * w)
+    assert torch.allclose(out, expected, atol=1e-14)
+
+
+def test_dot_product_closed_form():
+    ins = [(0, 0, 0, "uuu", True)]
+    x, y, w, src, dst = problem("8x1o", "8x1o", "8x0e", ins, 6, 20, 2)
+    out = conv("8x1o", "8x1o", "8x0e", ins, x, y, w, src, dst, 6)
+    msg = (x[src].reshape(20, 8, 3) * y.reshape(20, 8, 3)).sum(-1) * w / math.sqrt(3)
+    assert torch.allclose(out, torch.zeros(6, 8, dtype=torch.float64).index_add(0, dst, msg), atol=1e-13)
+    unweighted = [(0, 0, 0, "uuu", False)]
+    out = conv("8x1o", "8x1o", "8x0e", unweighted, x, y, w[:, :0], src, dst, 6)
+    msg = (x[src].reshape(20, 8, 3) * y.reshape(20, 8, 3)).sum(-1) / math.sqrt(3)
+    assert torch.allclose(out, torch.zeros(6, 8, dtype=torch.float64).index_add(0, dst, msg), atol=1e-13)
+
+
+def test_broadcast_edge_features_equal_uvu():
+    ch = 5
+    in1 = f"{ch}x0e+{ch}x1o+{ch}x2e"
+    edge = "1x0e+1x1o+1x2e"
+    edge_uuu = f"{ch}x0e+{ch}x1o+{ch}x2e"
+    uuu = uuu_paths(in1, edge_uuu, in1)
+    uvu = [(i, j, k, "uvu", True) for i, j, k, _, _ in uuu]
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(4, dims(in1)[0], generator=gen, dtype=torch.float64)
+    ysh = torch.randn(10, dims(edge)[0], generator=gen, dtype=torch.float64)
+    # repeat each l-block of the single-channel edge features over the ch channels
+    blocks, at = [], 0
+    for l in range(3):
+        blocks.append(ysh[:, at: at + 2 * l + 1].repeat(1, ch))
+        at += 2 * l + 1
+    y = torch.cat(blocks, 1)
+    w = torch.randn(10, ch * len(uuu), generator=gen, dtype=torch.float64)
+    src = torch.randint(4, (10,), generator=gen)
+    dst = torch.sort(torch.randint(4, (10,), generator=gen))[0]
+    a = conv(in1, edge_uuu, in1, uuu, x, y, w, src, dst, 4)
+    b = conv(in1, edge, in1, uvu, x, ysh, w, src, dst, 4)
+    assert torch.allclose(a, b, atol=1e-12)
+
+
+def test_oracle_equivariance():
+    ir = "4x0e+4x1o+4x2e"
+    instructions = uuu_paths(ir, ir, ir)
+    x, y, w, src, dst = problem(ir, ir, ir, instructions, 6, 15, 4)
+    R = rotation(7)
+    D = block_diag_d(ir, R, np.random.default_rng(8))
+    out = conv(ir, ir, ir, instructions, x, y, w, src, dst, 6)
+    rotated = conv(ir, ir, ir, instructions, x @ D.T, y @ D.T, w, src, dst, 6)
+    assert torch.allclose(rotated, out @ D.T, atol=1e-10)
+
+
+def test_oracle_gradcheck():
+    ir = "2x0e+2x1o"
+    instructions = uuu_paths(ir, ir, ir, unweighted=(2,))
+    x, y, w, src, dst = problem(ir, ir, ir, instructions, 3, 6, 5)
+    leaves = [t.clone().requires_grad_() for t in (x, y, w)]
+    env = torch.rand(6, dtype=torch.float64, requires_grad=True)
+    fn = lambda a, b, c, e: conv(ir, ir, ir, instructions, a, b, c, src, dst, 3, env=e)  # noqa: E731
+    assert torch.autograd.gradcheck(fn, (*leaves, env))
+    assert torch.autograd.gradgradcheck(fn, (*leaves, env))
+
+
+def test_l0_features_are_scalar_messages():
+    ir = "3x0e+3x1o"
+    instructions = uuu_paths(ir, ir, ir)
+    x, y, w, src, dst = problem(ir, ir, ir, instructions, 4, 8, 6)
+    env = torch.rand(8, dtype=torch.float64)
+    out, l0 = conv(ir, ir, ir, instructions, x, y, w, src, dst, 4, env=env, return_l0=True)
+    # scalar outputs: (0e x 0e -> 0e) and (1o x 1o -> 0e), each 3 channels, in output order
+    assert l0.shape == (8, 6)
+    summed = torch.zeros(4, 3, dtype=torch.float64).index_add(0, dst, (l0[:, :3] + l0[:, 3:]) * env[:, None])
+    assert torch.allclose(summed, out[:, :3], atol=1e-13)
+
+
+# ---------------------------------------------------------------------------
+# Lowering and the C-ABI plan (no kernel launches)
+# ---------------------------------------------------------------------------
+
+def test_metadata_lowering():
+    from lunaequivariance_amd import TensorProductConfig
+    from lunaequivariance_amd.uuu_conv import build_uuu_conv_metadata
+
+    ir = "4x0e+4x1o"
+    instructions = uuu_paths(ir, ir, ir, unweighted=(1,))
+    tp = TensorProductConfig(ir, ir, ir, instructions, internal_weights=False, shared_weights=False)
+    meta = build_uuu_conv_metadata(tp)
+    specs = meta["generated_specs"]
+    assert meta["weight_numel"] == tp.weight_numel == 4 * (len(instructions) - 1)
+    assert [s["weight_offset"] for s in specs] == [0, 4, 4, 8, 12][: len(specs)]
+    assert [s["has_weight"] for s in specs][1] is False
+    assert all(s["channels"] == 4 for s in specs)
+    for s, ins in zip(specs, tp.instructions):
+        assert s["terms"] and all(abs(c) > 0 for *_, c in s["terms"])
+        assert s["path_weight"] == pytest.approx(ins.path_weight)
+
+
+def test_metadata_errors():
+    from lunaequivariance_amd import TensorProductConfig
+    from lunaequivariance_amd.uuu_conv import build_uuu_conv_metadata
+
+    with pytest.raises(AssertionError, match="UUU requires equal"):
+        TensorProductConfig("4x0e", "2x0e", "4x0e", [(0, 0, 0, "uuu", True)], internal_weights=False,
+                            shared_weights=False)
+    tp = TensorProductConfig("4x0e", "4x0e", "4x0e", [(0, 0, 0, "uvu", True)], internal_weights=False,
+                             shared_weights=False)
+    with pytest.raises(ValueError, match="connection_mode='uuu'"):
+        build_uuu_conv_metadata(tp)
+    tp = TensorProductConfig("4x0e", "4x0e", "4x0e", [(0, 0, 0, "uuu", True)], internal_weights=False,
+                             shared_weights=False)
+    with pytest.raises(ValueError, match="float32 or float64"):
+        build_uuu_conv_metadata(tp, coefficient_dtype=torch.float16)
+
+
+def test_api_dispatches_uuu():
+    import lunaequivariance_amd as lunaeq
+    from lunaequivariance_amd.uuu_conv import LunaTPUUUConv, build_uuu_conv_metadata
+
+    ir = "4x0e+4x1o"
+    instructions = uuu_paths(ir, ir, ir)
+    op = lunaeq.prepare_tensor_product(ir, ir, ir, instructions, convolution=True)
+    assert isinstance(op, LunaTPUUUConv) and op.mode == "uuu_conv"
+    module = lunaeq.TensorProductConv(ir, ir, ir, instructions, internal_weights=False, shared_weights=False)
+    assert module.mode == "uuu_conv" and isinstance(module.op, LunaTPUUUConv)
+    module.double()
+    assert module.op.compute_dtype == torch.float64
+    meta = build_uuu_conv_metadata(module.tp)
+    assert isinstance(lunaeq.TensorProductConv(meta, mode="uuu").op, LunaTPUUUConv)
+    assert isinstance(lunaeq.prepare_tensor_product(meta, convolution=True, mode="uuu"), LunaTPUUUConv)
+    from lunaequivariance_amd.ops import restore_operator
+
+    assert isinstance(restore_operator(op.torch_config), LunaTPUUUConv)
+
+
+def test_kernels_fail_loudly_on_cpu_tensors():
+    import lunaequivariance_amd as lunaeq
+
+    ir = "4x0e"
+    module = lunaeq.TensorProductConv(ir, ir, ir, [(0, 0, 0, "uuu", True)], internal_weights=False,
+                                      shared_weights=False)
+    graph = module.create_graph(torch.tensor([0]), torch.tensor([0]), 1)
+    with pytest.raises(RuntimeError, match="run on the GPU"):
+        module(torch.randn(1, 4), torch.randn(1, 4), torch.randn(1, 4), graph=graph)
+
+
+def test_native_plan_flags_and_spec_errors():
+    import ctypes
+
+    from lunaequivariance_amd import TensorProductConfig, _native
+    from lunaequivariance_amd.uuu_conv import NativeUuuPlan, build_uuu_conv_metadata, spec_text
+
+    if not _native.library_available():
+        pytest.skip("library not built")
+    in1, in2, out = "4x0e+4x1o", "4x0e+4x1o", "4x0e+4x1o+2x0e"
+    tp = TensorProductConfig(in1, in2, out, uuu_paths(in1, in2, out), internal_weights=False,
+                             shared_weights=False)
+    for dtype in (torch.float32, torch.float64):
+        plan = NativeUuuPlan(spec_text(build_uuu_conv_metadata(tp, dtype), dtype))
+        assert plan.out_zero and not plan.gx_zero and not plan.gy_zero and not plan.gw_zero
+        plan.precompile()
+    lib = _native.lib()
+    handle = ctypes.c_void_p()
+    bad = [
+        "LUNAUVU1 32 4 4 4 4 1 0\n0 0 0 0 4 1 1 1 -1 0\n",          # wrong header
+        "LUNAUUU1 32 4 4 4 4 1 0\n0 0 0 0 5 1 1 1 -1 0\n",          # block outside in1
+        "LUNAUUU1 32 8 8 8 8 2 0\n0 0 0 0 4 1 1 1 -1 0\n2 0 4 4 4 1 1 1 -1 0\n",  # overlapping x blocks
+        "LUNAUUU1 32 4 4 4 4 1 0\n0 0 0 0 4 1 1 1 -1 1 0 1 0 1.0\n",  # j outside d2
+        "LUNAUUU1 32 4 4 4 4 1 0\n0 0 0 0 4 1 1 1 0 0\n",            # l0 column without l0_dim
+    ]
+    for text in bad:
+        assert lib.luna_uuu_plan_create(text.encode(), None, ctypes.byref(handle)) != 0
+        assert lib.luna_last_error().decode().startswith("uuu spec")
+
+
+def test_weight_linear_part():
+    """Unweighted paths make the product affine in w: derivatives along a weight
+    direction use the operator restricted to weighted paths, same l0 columns."""
+    from lunaequivariance_amd import TensorProductConfig
+    from lunaequivariance_amd.ops import restore_operator
+    from lunaequivariance_amd.uuu_conv import create_uuu_conv_operator
+
+    ir = "4x0e+4x1o"
+    weighted = uuu_paths(ir, ir, ir)
+    tp = TensorProductConfig(ir, ir, ir, weighted, internal_weights=False, shared_weights=False)
+    op = create_uuu_conv_operator(tp)
+    assert op.weight_linear() is op
+    mixed = uuu_paths(ir, ir, ir, unweighted=(0, 3))
+    tp = TensorProductConfig(ir, ir, ir, mixed, internal_weights=False, shared_weights=False)
+    op = create_uuu_conv_operator(tp)
+    lin = op.weight_linear()
+    assert lin is not op and lin is op.weight_linear()
+    assert len(lin.active_specs) == len(mixed) - 2 and lin.l0_dim == op.l0_dim
+    assert int(lin.spec.split()[6]) == len(mixed) - 2
+    assert not lin.l0_complete and op.l0_complete
+    assert restore_operator(lin.torch_config).active_specs == lin.active_specs
