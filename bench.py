@@ -35,6 +35,11 @@ CONFIGS = {
     "cfg3": dict(channels=128, atoms=20000, dtype="float64", double_backward=False),
     "cfg4": dict(channels=64, atoms=10000, dtype="float32", double_backward=True),
     "cfg5": dict(channels=64, rows=200000, dtype="float32"),
+    # UUU conv (the reference's UUU benchmark layout, docs/operators/tensor_product.md:255-275):
+    # 2,083 atoms, ~85,900 edges, 64 channels per degree on both inputs, per-edge weights.
+    "uuu_l2": dict(channels=64, atoms=2083, lmax=2, dtype="float32"),
+    "uuu_l3": dict(channels=64, atoms=2083, lmax=3, dtype="float32"),
+    "uuu_l4": dict(channels=64, atoms=2083, lmax=4, dtype="float32"),
 }
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
@@ -79,6 +84,9 @@ def main():
 
     if args.config == "cfg5":
         bench_uvw(args)
+        return
+    if args.config.startswith("uuu"):
+        bench_uuu(args)
         return
 
     cfg = CONFIGS[args.config]
@@ -253,6 +261,118 @@ def bench_uvw(args):
                    "rows": rows, "weight_numel": tp.weight_numel, "parallelism": "single GPU"},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "kernels": per_kernel, "cpu_baseline": cpu,
+    }))
+
+
+def uuu_algorithmic_bytes(N, E, in1, in2, out, wnum, real, index=4):
+    """Compulsory bytes of the UUU kernels, each tensor read or written once."""
+    X, Y, W, O = N * in1 * real, E * in2 * real, E * wnum * real, N * out * real
+    return {"uuu_fwd": X + Y + W + O + E * index + (N + 1) * 2 * index,
+            "uuu_bwd": (X + Y + W + O) + (X + Y + W) + 2 * E * index + (N + 1) * 2 * index}
+
+
+def bench_uuu(args):
+    """UUU conv: every allowed uuu path up to lmax on 64 channels per degree, x and
+    edge features of the same irreps, per-edge weights; one step = forward +
+    backward to x, edge features and weights (atoms/s, the reference's unit).
+    Also times the forward alone and a force-style step (+ double backward)."""
+    import torch
+
+    import lunaequivariance_amd as lunaeq
+    from lunaequivariance_amd import _native
+    from lunaequivariance_amd.workloads import periodic_radius_graph
+
+    cfg = CONFIGS[args.config]
+    dtype = getattr(torch, cfg["dtype"])
+    real = torch.finfo(dtype).bits // 8
+    device = torch.device("cuda:0")
+    torch.manual_seed(0)
+    ch, lmax, N = cfg["channels"], cfg["lmax"], cfg["atoms"]
+    ir = "+".join(f"{ch}x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(lmax + 1))
+    a = lunaeq.Irreps(ir)
+    instructions = [(i, j, k, "uuu", True) for i, (_, p) in enumerate(a) for j, (_, q) in enumerate(a)
+                    for k, (_, r) in enumerate(a) if r in p * q]
+    conv = lunaeq.TensorProductConv(ir, ir, ir, instructions, internal_weights=False, shared_weights=False,
+                                    dtype=dtype)
+    # density 0.0787 atoms/A^3 and a 5 A cutoff give ~41 neighbours per atom
+    src, dst, *_ = periodic_radius_graph(N, 0.0787, 5.0, seed=0, device=device)
+    E = src.numel()
+    graph = conv.create_graph(src, dst, N)
+    x = torch.randn(N, a.dim, device=device, dtype=dtype, requires_grad=True)
+    y = torch.randn(E, a.dim, device=device, dtype=dtype, requires_grad=True)
+    w = (torch.randn(E, conv.weight_numel, device=device, dtype=dtype) / len(instructions) ** 0.5).requires_grad_()
+    g = torch.randn(N, a.dim, device=device, dtype=dtype)
+
+    def forward():
+        with torch.no_grad():
+            return conv(x, y, w, graph=graph)
+
+    def step():
+        out = conv(x, y, w, graph=graph)
+        return (out, *torch.autograd.grad(out, (x, y, w), g))
+
+    def force_step():
+        out = conv(x, y, w, graph=graph)
+        gx, gy, gw = torch.autograd.grad(out, (x, y, w), g, create_graph=True)
+        return torch.autograd.grad(gx, (y, w), torch.ones_like(gx))
+
+    def timed(fn, steps, profile=False):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        if profile:
+            _native.profile_enable(True)
+            _native.profile_collect()
+        start = time.perf_counter()
+        for _ in range(steps):
+            result = fn()
+            del result
+        torch.cuda.synchronize()
+        elapsed = (time.perf_counter() - start) * 1000.0 / steps
+        kernels = None
+        if profile:
+            _native.profile_enable(False)
+            kernels = _native.profile_collect()
+        return elapsed, kernels
+
+    ms_step, kernels = timed(step, args.steps, profile=True)
+    ms_fwd, _ = timed(forward, args.steps)
+    ms_force, _ = timed(force_step, max(1, args.steps // 2))
+    algo = uuu_algorithmic_bytes(N, E, a.dim, a.dim, a.dim, conv.weight_numel, real)
+    per_kernel = {}
+    for name, (count, total, low, high) in kernels.items():
+        avg = total / count
+        entry = {"launches": count, "avg_ms": round(avg, 4), "min_ms": round(low, 4), "max_ms": round(high, 4)}
+        if name in algo:
+            launches_per_step = count / args.steps
+            entry["algorithmic_bytes_per_step"] = algo[name]
+            entry["gbs"] = round(algo[name] / (total / args.steps / 1000.0) / 1e9, 1)
+            entry["launches_per_step"] = launches_per_step
+        per_kernel[name] = entry
+    dominant = max(algo, key=lambda n: kernels.get(n, (0, 0))[1])
+    achieved = per_kernel[dominant]["gbs"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(ir, ir, ir, instructions, x, y, w, g, src, dst, N, 40, dtype)
+    print(json.dumps({
+        "metric": "UUU TP-conv atoms/s fwd+bwd", "value": round(N / (ms_step / 1000.0), 1), "unit": "atoms/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32" if dtype == torch.float32 else "f64",
+        "data": "synthetic (periodic random atoms, radius graph, random features and per-edge weights)",
+        "config": {"workload": f"{args.config}: UUU conv, {ch} channels per degree, lmax={lmax}, every uuu path, "
+                               f"{N} atoms, {E} edges, per-edge weights, fwd+bwd",
+                   "num_nodes": N, "num_edges": E, "weight_numel": conv.weight_numel,
+                   "paths": len(instructions), "parallelism": "single GPU"},
+        "forward_atoms_per_s": round(N / (ms_fwd / 1000.0), 1),
+        "forward_ms": round(ms_fwd, 4),
+        "backward_atoms_per_s": round(N / ((ms_step - ms_fwd) / 1000.0), 1),
+        "double_backward_step_ms": round(ms_force, 4),
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(args.config, dtype, dominant),
+                     "algorithmic_bytes": algo[dominant]},
         "kernels": per_kernel, "cpu_baseline": cpu,
     }))
 

@@ -349,8 +349,7 @@ __device__ __forceinline__ double lane_xor(double v) {
 
 // Components of each block a group reads, from its terms.
 struct Uses {
-  std::set<std::pair<int, int>> x, y, o;           // (block, component)
-  std::set<std::tuple<int, int, int, int>> xy;     // (xb, i, yb, j)
+  std::set<std::pair<int, int>> x, y, o;  // (block, component)
 };
 
 Uses uses_of(const USpec& s, const UGroup& g) {
@@ -361,15 +360,11 @@ Uses uses_of(const USpec& s, const UGroup& g) {
       u.x.insert({q.xb, t.i});
       u.y.insert({q.yb, t.j});
       u.o.insert({q.ob, t.k});
-      u.xy.insert({q.xb, t.i, q.yb, t.j});
     }
   }
   return u;
 }
 
-std::string xy_name(int xb, int i, int yb, int j) {
-  return "xy" + std::to_string(xb) + "_" + std::to_string(i) + "_" + std::to_string(yb) + "_" + std::to_string(j);
-}
 
 // Emits `real name = sum_n a_n * b_n` as one multiply and a chain of FMAs.
 void fma_sum(Code& c, const std::string& name, const std::vector<std::pair<std::string, std::string>>& products) {
@@ -391,13 +386,33 @@ void lane_sum(Code& c, const std::vector<std::string>& names, int from, int to, 
     for (const std::string& n : names) c.line("%s%s += lane_xor<%d>(%s);", indent, n.c_str(), m, n.c_str());
 }
 
-// Kernel head shared by both directions: wave -> (node, slot), lane -> (sub, u).
+// Kernel head shared by both directions: workgroup -> (node, chunk); its
+// `split` waves take interleaved runs of the node's edges; lane -> (sub, u).
 void emit_head(Code& c, const char* order_name, int slots) {
-  c.line("  const i64 item = (i64)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
-  c.line("  if (item >= items) return;");
+  c.line("  const int item = blockIdx.x;");
+  c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
   c.line("  const int lane = threadIdx.x & 63;");
-  c.line("  const int slot = (int)(item %% %d);", slots);
+  c.line("  const int slot = item %% %d;", slots);
   c.line("  const int node = %s[item / %d];", order_name, slots);
+}
+
+// Sums `names` over the waves of the workgroup through LDS (halving tree);
+// wave 0 ends with the totals.  Every wave of the workgroup executes it.
+void block_sum(Code& c, const std::vector<std::string>& names) {
+  const int n = (int)names.size();
+  c.line("    if (split > 1) {");
+  c.line("      real* red = reinterpret_cast<real*>(lds);");
+  c.line("      for (int h = split >> 1; h > 0; h >>= 1) {");
+  c.line("        if (wave >= h && wave < 2 * h) {");
+  for (int a = 0; a < n; ++a) c.line("          red[((wave - h) * %d + %d) * 64 + lane] = %s;", n, a, names[a].c_str());
+  c.line("        }");
+  c.line("        __syncthreads();");
+  c.line("        if (wave < h) {");
+  for (int a = 0; a < n; ++a) c.line("          %s += red[(wave * %d + %d) * 64 + lane];", names[a].c_str(), n, a);
+  c.line("        }");
+  c.line("        __syncthreads();");
+  c.line("      }");
+  c.line("    }");
 }
 
 void emit_group_lanes(Code& c, const UGroup& g) {
@@ -409,6 +424,56 @@ void emit_group_lanes(Code& c, const UGroup& g) {
   c.line("    const bool act = u < %d;", g.ch);
 }
 
+// t{p}_k = sum_{(i,j,k)} c x_i y_j of path p, as sum_i x_i z_ik.
+void emit_t(Code& c, const USpec& s, int p) {
+  const UPath& q = s.paths[p];
+  std::map<int, std::map<int, std::vector<const UTerm*>>> by_ik;  // i -> k -> terms
+  std::set<int> ks;
+  for (const UTerm& t : q.terms) {
+    by_ik[t.i][t.k].push_back(&t);
+    ks.insert(t.k);
+  }
+  for (int k : ks) c.line("        real t%d_%d = 0;", p, k);
+  for (const auto& ik : by_ik)
+    for (const auto& kv : ik.second) {
+      std::vector<std::pair<std::string, std::string>> products;
+      for (const UTerm* t : kv.second) products.push_back({lit(t->c, s.bits), "y" + sfx(q.yb, t->j)});
+      const std::string z = "z" + std::to_string(p) + "_" + sfx(ik.first, kv.first);
+      fma_sum(c, z, products);
+      c.line("        t%d_%d = FMA(x%d_%d, %s, t%d_%d);", p, kv.first, q.xb, ik.first, z.c_str(), p, kv.first);
+    }
+}
+
+// r{tag}{p}_ij = sum_k c_ijk seed(k), then sx{tag}{p}_i = sum_j y_j r_ij,
+// sy{tag}{p}_j = sum_i x_i r_ij and S{tag}{p} = sum_i x_i sx_i as requested.
+void emit_r_sums(Code& c, const USpec& s, int p, const std::string& tag, const std::function<std::string(int)>& seed,
+                 bool want_sx, bool want_sy, bool want_s) {
+  const UPath& q = s.paths[p];
+  const std::string P = tag + std::to_string(p);
+  std::map<std::pair<int, int>, std::vector<const UTerm*>> by_ij;
+  for (const UTerm& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
+  std::map<int, std::vector<std::pair<std::string, std::string>>> rows, cols;
+  for (const auto& kv : by_ij) {
+    const int i = kv.first.first, j = kv.first.second;
+    std::vector<std::pair<std::string, std::string>> products;
+    for (const UTerm* t : kv.second) products.push_back({lit(t->c, s.bits), seed(t->k)});
+    const std::string r = "r" + P + "_" + sfx(i, j);
+    fma_sum(c, r, products);
+    rows[i].push_back({"y" + sfx(q.yb, j), r});
+    cols[j].push_back({"x" + sfx(q.xb, i), r});
+  }
+  std::vector<std::pair<std::string, std::string>> total;
+  if (want_sx || want_s)
+    for (const auto& kv : rows) {
+      const std::string name = "sx" + P + "_" + std::to_string(kv.first);
+      fma_sum(c, name, kv.second);
+      total.push_back({"x" + sfx(q.xb, kv.first), name});
+    }
+  if (want_sy)
+    for (const auto& kv : cols) fma_sum(c, "sy" + P + "_" + std::to_string(kv.first), kv.second);
+  if (want_s) fma_sum(c, "S" + P, total);
+}
+
 std::string emit_forward(const UuuPlan& plan, bool env, bool l0) {
   const USpec& s = plan.spec;
   Code c;
@@ -417,10 +482,11 @@ std::string emit_forward(const UuuPlan& plan, bool env, bool l0) {
     const UGroup& g = plan.fwd[gi];
     const Uses use = uses_of(s, g);
     const int nsub = 64 / g.cw;
-    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uuu_fwd_g%d(", (int)gi);
+    c.line("extern \"C\" __global__ void __launch_bounds__(512) luna_uuu_fwd_g%d(", (int)gi);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
     c.line("    const real* __restrict__ env, const int* __restrict__ src, const int* __restrict__ rowptr,");
-    c.line("    const int* __restrict__ order, real* __restrict__ out, real* __restrict__ l0, i64 items) {");
+    c.line("    const int* __restrict__ order, real* __restrict__ out, real* __restrict__ l0, int split) {");
+    c.line("  extern __shared__ __align__(16) unsigned char lds[];");
     emit_head(c, "order", g.chunks);
     c.line("  const int beg = rowptr[node], end = rowptr[node + 1];");
     c.line("  {");
@@ -431,7 +497,7 @@ std::string emit_forward(const UuuPlan& plan, bool env, bool l0) {
         accs.push_back("o" + std::to_string(b) + "_" + std::to_string(k));
         c.line("    real %s = 0;", accs.back().c_str());
       }
-    c.line("    for (int e0 = beg; e0 < end; e0 += %d) {", nsub);
+    c.line("    for (int e0 = beg + wave * %d; e0 < end; e0 += %d * split) {", nsub, nsub);
     c.line("      const int e = e0 + sub;");
     c.line("      if (act && e < end) {");
     c.line("        const i64 sn = src[e];");
@@ -447,38 +513,37 @@ std::string emit_forward(const UuuPlan& plan, bool env, bool l0) {
     for (int p : g.paths)
       if (s.paths[p].w_off >= 0)
         c.line("        const real w%d = __builtin_nontemporal_load(w + (i64)e * WNUM + %d + u);", p, s.paths[p].w_off);
-    for (const auto& q : use.xy) {
-      const auto [xb, i, yb, j] = q;
-      c.line("        const real %s = x%d_%d * y%d_%d;", xy_name(xb, i, yb, j).c_str(), xb, i, yb, j);
-    }
+    // t_k = sum_i x_i z_ik with z_ik = sum_j c_ijk y_j: one FMA per term and
+    // one per (i, k), and nothing lives beyond its path.
     for (int p : g.paths) {
       const UPath& q = s.paths[p];
-      std::map<int, std::vector<const UTerm*>> by_k;
-      for (const UTerm& t : q.terms) by_k[t.k].push_back(&t);
-      if (by_k.empty()) continue;
+      if (q.terms.empty()) {
+        if (l0 && q.l0_col >= 0) c.line("        l0[(i64)e * L0DIM + %d + u] = 0;", q.l0_col);
+        continue;
+      }
+      emit_t(c, s, p);
+      std::set<int> ks;
+      for (const UTerm& t : q.terms) ks.insert(t.k);
       std::string scale = q.w_off >= 0 ? "w" + std::to_string(p) : "";
       if (env) scale = scale.empty() ? "ev" : "ev * " + scale;
       if (!scale.empty()) c.line("        const real a%d = %s;", p, scale.c_str());
-      for (const auto& kv : by_k) {
-        std::vector<std::pair<std::string, std::string>> products;
-        for (const UTerm* t : kv.second) products.push_back({lit(t->c, s.bits), xy_name(q.xb, t->i, q.yb, t->j)});
-        fma_sum(c, "t" + sfx(p, kv.first), products);
+      for (int k : ks) {
         if (scale.empty())
-          c.line("        o%d_%d += t%d_%d;", q.ob, kv.first, p, kv.first);
+          c.line("        o%d_%d += t%d_%d;", q.ob, k, p, k);
         else
-          c.line("        o%d_%d = FMA(a%d, t%d_%d, o%d_%d);", q.ob, kv.first, p, p, kv.first, q.ob, kv.first);
+          c.line("        o%d_%d = FMA(a%d, t%d_%d, o%d_%d);", q.ob, k, p, p, k, q.ob, k);
       }
       if (l0 && q.l0_col >= 0) {
-        const bool has0 = by_k.count(0) > 0;
-        std::string v = has0 ? "t" + std::to_string(p) + "_0" : "(real)0";
-        if (q.w_off >= 0 && has0) v = "w" + std::to_string(p) + " * " + v;
+        std::string v = ks.count(0) ? "t" + std::to_string(p) + "_0" : "(real)0";
+        if (q.w_off >= 0 && ks.count(0)) v = "w" + std::to_string(p) + " * " + v;
         c.line("        l0[(i64)e * L0DIM + %d + u] = %s;", q.l0_col, v.c_str());
       }
     }
     c.line("      }");
     c.line("    }");
     if (nsub > 1) lane_sum(c, accs, g.cw, 32, "    ");
-    c.line("    if (sub == 0 && act) {");
+    block_sum(c, accs);
+    c.line("    if (wave == 0 && sub == 0 && act) {");
     c.line("      real* orow = out + (i64)node * OUTD;");
     for (int b : g.obs)
       for (int k = 0; k < s.oblocks[b].d; ++k)
@@ -499,12 +564,13 @@ std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx,
     const UGroup& g = plan.bwd[gi];
     const Uses use = uses_of(s, g);
     const int nsub = 64 / g.cw;
-    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uuu_bwd_g%d(", (int)gi);
+    c.line("extern \"C\" __global__ void __launch_bounds__(512) luna_uuu_bwd_g%d(", (int)gi);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ w,");
     c.line("    const real* __restrict__ env, const real* __restrict__ g, const real* __restrict__ gl0,");
     c.line("    const int* __restrict__ dst, const int* __restrict__ rowptr, const int* __restrict__ edge_ids,");
     c.line("    const int* __restrict__ order, real* __restrict__ gx, real* gy, real* __restrict__ gw,");
-    c.line("    real* __restrict__ part, i64 items, i64 num_edges) {");
+    c.line("    real* __restrict__ part, int split, i64 num_edges) {");
+    c.line("  extern __shared__ __align__(16) unsigned char lds[];");
     emit_head(c, "order", g.chunks);
     c.line("  const int beg = rowptr[node], end = rowptr[node + 1];");
     c.line("  {");
@@ -523,7 +589,7 @@ std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx,
           gxs.push_back("gx" + std::to_string(b) + "_" + std::to_string(i));
           c.line("    real %s = 0;", gxs.back().c_str());
         }
-    c.line("    for (int e0 = beg; e0 < end; e0 += %d) {", nsub);
+    c.line("    for (int e0 = beg + wave * %d; e0 < end; e0 += %d * split) {", nsub, nsub);
     c.line("      const int pos = e0 + sub;");
     c.line("      const int e = pos < end ? edge_ids[pos] : 0;");
     if (want_genv) c.line("      real gev = 0;");
@@ -535,93 +601,71 @@ std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx,
     for (const auto& ok : use.o)
       c.line("        const real g%d_%d = g[dn * OUTD + %d + (i64)u * %d];", ok.first, ok.second,
              s.oblocks[ok.first].off + ok.second, s.oblocks[ok.first].d);
-    if (env) {
-      c.line("        const real ev = env[e];");
-      for (const auto& ok : use.o) c.line("        const real G%d_%d = ev * g%d_%d;", ok.first, ok.second, ok.first, ok.second);
-    } else {
-      for (const auto& ok : use.o) c.line("        const real G%d_%d = g%d_%d;", ok.first, ok.second, ok.first, ok.second);
-    }
+    if (env) c.line("        const real ev = env[e];");
     for (int p : g.paths)
       if (s.paths[p].w_off >= 0 && (want_gx || want_gy || want_genv))
         c.line("        const real w%d = __builtin_nontemporal_load(w + (i64)e * WNUM + %d + u);", p, s.paths[p].w_off);
-    const bool need_xy = want_gw || want_genv;
-    if (need_xy)
-      for (const auto& q : use.xy) {
-        const auto [xb, i, yb, j] = q;
-        c.line("        const real %s = x%d_%d * y%d_%d;", xy_name(xb, i, yb, j).c_str(), xb, i, yb, j);
-      }
     if (want_gy)
       for (int b : g.ybs)
         for (int j = 0; j < s.yblocks[b].d; ++j) c.line("        real gy%d_%d = 0;", b, j);
+    // Per path, with r_ij = sum_k c_ijk seed_k:
+    //   sx_i = sum_j y_j r_ij (gx), sy_j = sum_i x_i r_ij (gy), S = sum_i x_i sx_i (gw).
+    // The seed is the raw g and the scale env * w is applied to the sums, except
+    // on scalar paths with an l0 seed, whose seed is env * g + gl0.
     for (int p : g.paths) {
       const UPath& q = s.paths[p];
+      const std::string P = std::to_string(p);
       if (q.terms.empty()) {
         if (want_gw && q.w_off >= 0)
           c.line("        __builtin_nontemporal_store((real)0, gw + (i64)e * WNUM + %d + u);", q.w_off);
         continue;
       }
       const bool l0path = gl0 && q.l0_col >= 0;
-      // Seeds of this path: G (env * g), plus the scalar-feature seed.
-      auto seed = [&](int k) {
-        std::string name = "G" + std::to_string(q.ob) + "_" + std::to_string(k);
-        return (l0path && k == 0) ? std::string("Gl") + std::to_string(p) : name;
+      const std::string w = q.w_off >= 0 ? "w" + P : "";
+      auto raw = [&](int k) { return "g" + sfx(q.ob, k); };
+      std::string seed0;
+      if (l0path) {
+        c.line("        const real Gl%d = %s + gl0[(i64)e * L0DIM + %d + u];", p,
+               env ? ("ev * " + raw(0)).c_str() : raw(0).c_str(), q.l0_col);
+        seed0 = "Gl" + P;
+      }
+      // Scale of the sums: w * env for raw seeds, w for the l0 seed.
+      std::string scale = w;
+      if (env && !l0path) scale = scale.empty() ? "ev" : "ev * " + scale;
+      if (!scale.empty() && (want_gx || want_gy)) c.line("        const real a%d = %s;", p, scale.c_str());
+      const bool need_s = want_gw || (want_genv && !l0path);
+      emit_r_sums(c, s, p, "", [&](int k) { return (l0path && k == 0) ? seed0 : raw(k); }, want_gx || need_s,
+                  want_gy, need_s);
+      auto add = [&](const char* acc, int blk, int idx, const std::string& v) {
+        if (scale.empty())
+          c.line("        %s%d_%d += %s;", acc, blk, idx, v.c_str());
+        else
+          c.line("        %s%d_%d = FMA(a%d, %s, %s%d_%d);", acc, blk, idx, p, v.c_str(), acc, blk, idx);
       };
-      if (l0path)
-        c.line("        const real Gl%d = G%d_0 + gl0[(i64)e * L0DIM + %d + u];", p, q.ob, q.l0_col);
-      // r_ij = sum_k c_ijk seed_k
-      std::map<std::pair<int, int>, std::vector<const UTerm*>> by_ij;
-      for (const UTerm& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
-      for (const auto& kv : by_ij) {
-        std::vector<std::pair<std::string, std::string>> products;
-        for (const UTerm* t : kv.second) products.push_back({lit(t->c, s.bits), seed(t->k)});
-        fma_sum(c, "r" + std::to_string(p) + "_" + sfx(kv.first.first, kv.first.second), products);
+      std::set<int> is, js;
+      for (const UTerm& t : q.terms) {
+        is.insert(t.i);
+        js.insert(t.j);
       }
-      auto r_name = [&](int i, int j) { return "r" + std::to_string(p) + "_" + sfx(i, j); };
-      const std::string a = q.w_off >= 0 ? "w" + std::to_string(p) : "";
+      if (want_gx)
+        for (int i : is) add("gx", q.xb, i, "sx" + P + "_" + std::to_string(i));
+      if (want_gy)
+        for (int j : js) add("gy", q.yb, j, "sy" + P + "_" + std::to_string(j));
       if (want_gw && q.w_off >= 0) {
-        std::vector<std::pair<std::string, std::string>> products;
-        for (const auto& kv : by_ij)
-          products.push_back({xy_name(q.xb, kv.first.first, q.yb, kv.first.second), r_name(kv.first.first, kv.first.second)});
-        fma_sum(c, "gw" + std::to_string(p), products);
-        c.line("        __builtin_nontemporal_store(gw%d, gw + (i64)e * WNUM + %d + u);", p, q.w_off);
-      }
-      // gx_i += a * sum_j y_j r_ij and gy_j += a * sum_i x_i r_ij
-      for (int side = 0; side < 2; ++side) {
-        if ((side == 0 && !want_gx) || (side == 1 && !want_gy)) continue;
-        std::map<int, std::vector<std::pair<std::string, std::string>>> sums;
-        for (const auto& kv : by_ij) {
-          const int i = kv.first.first, j = kv.first.second;
-          if (side == 0)
-            sums[i].push_back({"y" + sfx(q.yb, j), r_name(i, j)});
-          else
-            sums[j].push_back({"x" + sfx(q.xb, i), r_name(i, j)});
-        }
-        const int blk = side == 0 ? q.xb : q.yb;
-        const char* acc = side == 0 ? "gx" : "gy";
-        for (const auto& kv : sums) {
-          const std::string tmp = std::string(side == 0 ? "sx" : "sy") + std::to_string(p) + "_" + std::to_string(kv.first);
-          fma_sum(c, tmp, kv.second);
-          if (a.empty())
-            c.line("        %s%d_%d += %s;", acc, blk, kv.first, tmp.c_str());
-          else
-            c.line("        %s%d_%d = FMA(%s, %s, %s%d_%d);", acc, blk, kv.first, a.c_str(), tmp.c_str(), acc, blk,
-                   kv.first);
-        }
+        const std::string v = (env && !l0path) ? "ev * S" + P : "S" + P;
+        c.line("        __builtin_nontemporal_store(%s, gw + (i64)e * WNUM + %d + u);", v.c_str(), q.w_off);
       }
       if (want_genv) {
-        // d out / d env = a * sum_k t_k g_k with t_k = sum c x_i y_j and the raw seed g.
-        std::map<int, std::vector<std::pair<std::string, std::string>>> by_k;
-        for (const UTerm& t : q.terms) by_k[t.k].push_back({lit(t.c, s.bits), xy_name(q.xb, t.i, q.yb, t.j)});
-        std::vector<std::pair<std::string, std::string>> dots;
-        for (const auto& kv : by_k) {
-          fma_sum(c, "t" + sfx(p, kv.first), kv.second);
-          dots.push_back({"t" + sfx(p, kv.first), "g" + sfx(q.ob, kv.first)});
+        // d out / d env = w * sum_ijk c x_i y_j g_k with the raw seed.
+        std::string total = "S" + P;
+        if (l0path) {
+          emit_r_sums(c, s, p, "0", raw, true, false, true);
+          total = "S0" + P;
         }
-        fma_sum(c, "ge" + std::to_string(p), dots);
-        if (a.empty())
-          c.line("        gev += ge%d;", p);
+        if (w.empty())
+          c.line("        gev += %s;", total.c_str());
         else
-          c.line("        gev = FMA(%s, ge%d, gev);", a.c_str(), p);
+          c.line("        gev = FMA(%s, %s, gev);", w.c_str(), total.c_str());
       }
     }
     if (want_gy)
@@ -643,7 +687,8 @@ std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx,
     c.line("    }");
     if (want_gx) {
       if (nsub > 1) lane_sum(c, gxs, g.cw, 32, "    ");
-      c.line("    if (sub == 0 && act) {");
+      block_sum(c, gxs);
+      c.line("    if (wave == 0 && sub == 0 && act) {");
       c.line("      real* xrow = gx + (i64)node * IN1;");
       for (int b : g.xbs)
         for (int i = 0; i < s.xblocks[b].d; ++i)
@@ -678,9 +723,20 @@ void check_sizes(int64_t num_nodes, int64_t num_edges) {
 }
 
 unsigned blocks_for(int64_t items) {
-  const int64_t blocks = (items + 3) / 4;
-  if (blocks > 0x7fffffffLL) fail("uuu: launch grid exceeds 2^31 workgroups");
-  return (unsigned)blocks;
+  if (items > 0x7fffffffLL) fail("uuu: launch grid exceeds 2^31 workgroups");
+  return (unsigned)items;
+}
+
+// Waves per workgroup sharing one node's edges: enough workgroups times waves
+// to give every SIMD of the chip about eight waves, at most 8 per node.
+int split_for(int64_t workgroups) {
+  int split = 1;
+  while (split < 8 && workgroups * split < 8192) split *= 2;
+  return split;
+}
+
+size_t lds_bytes(int split, int accumulators, int bits) {
+  return split > 1 ? (size_t)(split / 2) * accumulators * 64 * (bits / 8) : 0;
 }
 
 }  // namespace
@@ -766,10 +822,14 @@ int luna_uuu_conv_fwd(const LunaUuuPlan* cplan, const void* x, const void* y, co
     const std::string v = std::string("fwd") + (env ? '1' : '0') + (l0 ? '1' : '0');
     hipModule_t module = p.kernels.module_for(v, [&] { return source_for(p, v); });
     for (size_t gi = 0; gi < p.fwd.size(); ++gi) {
-      int64_t items = num_nodes * p.fwd[gi].chunks;
-      void* args[] = {&x, &y, &w, &env, &src, &dst_rowptr, &node_order, &out, &l0, &items};
+      const UGroup& g = p.fwd[gi];
+      const int64_t items = num_nodes * g.chunks;
+      int split = split_for(items);
+      int accs = 0;
+      for (int b : g.obs) accs += p.spec.oblocks[b].d;
+      void* args[] = {&x, &y, &w, &env, &src, &dst_rowptr, &node_order, &out, &l0, &split};
       launch("uuu_fwd", function_for(module, "luna_uuu_fwd_g" + std::to_string(gi)), dim3(blocks_for(items)),
-             dim3(256), (hipStream_t)stream, args);
+             dim3(64 * split), (hipStream_t)stream, args, (unsigned)lds_bytes(split, accs, p.spec.bits));
     }
   });
 }
@@ -818,11 +878,16 @@ int luna_uuu_conv_bwd(const LunaUuuPlan* cplan, const void* x, const void* y, co
     const std::string v = "bwd" + flags;
     hipModule_t module = p.kernels.module_for(v, [&] { return source_for(p, v); });
     for (size_t gi = 0; gi < p.bwd.size(); ++gi) {
-      int64_t items = num_nodes * p.bwd[gi].chunks;
+      const UGroup& grp = p.bwd[gi];
+      const int64_t items = num_nodes * grp.chunks;
+      int split = split_for(items);
+      int accs = 0;
+      if (gx)
+        for (int b : grp.xbs) accs += p.spec.xblocks[b].d;
       void* args[] = {&x, &y, &w, &env, &g, &gl0, &dst, &src_rowptr, &edge_ids_by_src, &source_node_order,
-                      &gx, &gy, &gw, &part, &items, &E};
+                      &gx, &gy, &gw, &part, &split, &E};
       launch("uuu_bwd", function_for(module, "luna_uuu_bwd_g" + std::to_string(gi)), dim3(blocks_for(items)),
-             dim3(256), s, args);
+             dim3(64 * split), s, args, (unsigned)lds_bytes(split, accs, p.spec.bits));
     }
     if (genv && p.genv_slots > 1) {
       void* args[] = {&part, &genv, &E};

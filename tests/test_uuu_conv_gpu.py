@@ -222,3 +222,12 @@ def test_prebuilt_metadata_and_compile_op():
     c, _ = torch.ops.lunaeq_amd.uuu_conv_forward(x, y, w, None, ops.graph_tables(graph), 6, False,
                                                  prepared.torch_config)
     assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("nodes", [300, 3000, 9000])
+def test_waves_per_node(dtype, nodes):
+    """Few nodes give each node several waves (8 at 300 nodes, 4 at 3,000) that
+    split its edges and sum through LDS; 9,000 nodes run one wave per node."""
+    ir = "16x0e+16x1o"
+    run_case(ir, ir, ir, uuu_paths(ir, ir, ir), nodes, 4 * nodes, dtype, nodes, env=True, orders=1)
