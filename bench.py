@@ -51,6 +51,8 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--step-only", action="store_true",
+                        help="UUU configs: time only the fwd+bwd step (for profiler runs)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="only run a 2 GiB device-to-device copy (HBM counter calibration)")
     parser.add_argument("--cpu-shard", type=int, default=400,
@@ -337,8 +339,10 @@ def bench_uuu(args):
         return elapsed, kernels
 
     ms_step, kernels = timed(step, args.steps, profile=True)
-    ms_fwd, _ = timed(forward, args.steps)
-    ms_force, _ = timed(force_step, max(1, args.steps // 2))
+    ms_fwd = ms_force = float("nan")
+    if not args.step_only:
+        ms_fwd, _ = timed(forward, args.steps)
+        ms_force, _ = timed(force_step, max(1, args.steps // 2))
     algo = uuu_algorithmic_bytes(N, E, a.dim, a.dim, a.dim, conv.weight_numel, real)
     per_kernel = {}
     for name, (count, total, low, high) in kernels.items():
