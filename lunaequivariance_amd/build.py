@@ -89,12 +89,36 @@ def uvw_operators():
     return [LunaTPUVW(paths)]
 
 
+def uuu_operators():
+    """UUU convolutions of the benchmark (64 channels per degree, lmax 2-4, fp32)
+    and of the reference's standard test problem (fp32 and fp64)."""
+    import torch
+
+    from .irreps import Irreps
+    from .layout import TensorProductConfig
+    from .uuu_conv import create_uuu_conv_operator
+
+    def config(ir):
+        a = Irreps(ir)
+        paths = [(i, j, k, "uuu", True) for i, (_, x) in enumerate(a) for j, (_, y) in enumerate(a)
+                 for k, (_, z) in enumerate(a) if z in x * y]
+        return TensorProductConfig(ir, ir, ir, paths, internal_weights=False, shared_weights=False)
+
+    ops = []
+    for lmax in (2, 3, 4):
+        ir = "+".join(f"64x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(lmax + 1))
+        ops.append(create_uuu_conv_operator(config(ir), dtype=torch.float32))
+    for dtype in (torch.float32, torch.float64):
+        ops.append(create_uuu_conv_operator(config("32x0e+32x1o"), dtype=dtype))
+    return ops
+
+
 def precompile() -> int:
     from . import _native
 
     _native.check(_native.lib().luna_graph_precompile(_native.cache_dir().encode()), "luna_graph_precompile")
     count = 1
-    for op in standard_operators() + uvw_operators():
+    for op in standard_operators() + uvw_operators() + uuu_operators():
         op.plan.precompile()
         count += 1
     return count
