@@ -117,6 +117,8 @@ std::string prelude(const Spec& spec) {
   s << "#define IN2 " << spec.in2 << "LL\n";
   s << "#define OUTD " << spec.out << "LL\n";
   s << "#define WNUM " << spec.wnum << "LL\n";
+  // Row stride of the weights read per edge: 0 when one row serves every edge.
+  s << "#define WROW " << (spec.w_broadcast ? "0LL" : "WNUM") << "\n";
   s << "#define L0DIM " << spec.l0_dim << "LL\n";
   s << "#define PART_W " << spec.in2 + 1 << "LL\n";
   if (fp64) {
@@ -274,7 +276,7 @@ void emit_edge_loop(Code& c, const Spec& spec, const Group& g, const GroupUse& u
     c.line("      {");
     c.line("        const real* xq = x + (i64)%s * IN1 + (%d + uc * %d);", srcv, g.x_off, g.d1);
     for (int i = 0; i < g.d1; ++i) c.line("        %cx%d = xq[%d];", b, i, i);
-    c.line("        const real* wq = w + (i64)%s * WNUM;", edge);
+    c.line("        const real* wq = w + (i64)%s * WROW;", edge);
     for (int n = 0; n < np; ++n) {
       const Path& q = spec.paths[g.paths[n]];
       if (opt.nt_w)
@@ -327,7 +329,7 @@ void emit_edge_loop(Code& c, const Spec& spec, const Group& g, const GroupUse& u
     c.line("      const int s = src[e];");
     c.line("      const real* xr = x + (i64)s * IN1 + (%d + uc * %d);", g.x_off, g.d1);
     for (int i = 0; i < g.d1; ++i) c.line("      const real x%d = xr[%d];", i, i);
-    c.line("      const real* wr = w + (i64)e * WNUM;");
+    c.line("      const real* wr = w + (i64)e * WROW;");
     for (int n = 0; n < np; ++n) {
       const Path& q = spec.paths[g.paths[n]];
       c.line("      const real w%d = wr[%d + uc * %d];", n, q.w_off, q.w_stride);
@@ -733,7 +735,7 @@ std::string emit_forward(const Plan& plan, bool env, bool l0) {
   Options opt = options();
   opt.prefetch = opt.fwd_prefetch;
   opt.depth = opt.fwd_depth;
-  opt.nt_w = opt.fwd_nt_w;
+  opt.nt_w = opt.fwd_nt_w && !plan.spec.w_broadcast;
   if (opt.fwd_local < 0) opt.fwd_local = spec.dtype_bits == 64;
   Code c;
   c.raw(prelude(spec));

@@ -31,6 +31,7 @@ struct Path {
 struct Spec {
   int dtype_bits = 32;
   int in1 = 0, in2 = 0, out = 0, wnum = 0, l0_dim = 0;
+  bool w_broadcast = false;  // one weight row for every edge (no weight gradient)
   std::vector<Path> paths;
 };
 

@@ -142,6 +142,7 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
     if (num_edges > 0 && (!y || !w || !src || !edge_ids_by_src)) fail("luna_uvu_conv_bwd: null edge tensor");
     if (gl0 && plan.spec.l0_dim == 0) gl0 = nullptr;
     if (!env) genv = nullptr;
+    if (gw && plan.spec.w_broadcast) fail("luna_uvu_conv_bwd: a broadcast weight row has no per-edge gradient");
     int64_t E = num_edges;
     const bool want_parts = (gy || genv) && E > 0;
     const bool want_msg = gx && E > 0;

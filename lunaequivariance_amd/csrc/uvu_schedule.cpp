@@ -51,7 +51,7 @@ Spec parse_spec(const std::string& text) {
   std::istringstream in(text);
   std::string magic;
   in >> magic;
-  if (magic != "LUNAUVU1") fail("spec: missing LUNAUVU1 header");
+  if (magic != "LUNAUVU1" && magic != "LUNAUVU2") fail("spec: missing LUNAUVU1 header");
   Spec s;
   s.dtype_bits = read_int(in, "dtype");
   if (s.dtype_bits != 32 && s.dtype_bits != 64) fail("spec: dtype must be 32 or 64");
@@ -61,6 +61,8 @@ Spec parse_spec(const std::string& text) {
   s.wnum = read_int(in, "weight_numel");
   int npaths = read_int(in, "npaths");
   s.l0_dim = read_int(in, "l0_dim");
+  // LUNAUVU2 adds a flag: the weight operand is one row shared by every edge.
+  if (magic == "LUNAUVU2") s.w_broadcast = read_int(in, "w_broadcast") != 0;
   if (npaths <= 0) fail("spec: UVU convolution needs at least one path");
   for (int p = 0; p < npaths; ++p) {
     Path q;

@@ -1,10 +1,10 @@
 """Functional API: preparation and calls with explicit weights.
 
 Mirrors ``prepare_tensor_product`` / ``tensor_product_conv``
-(``src/lunatp/interface.py:147-262``) for the UVU and UUU convolutions and the
-shared-weight UVW product.  Other connection modes of the reference (uvw
-convolution, non-convolution uuu/uvu products) are outside this library's
-scope and raise ``NotImplementedError``.
+(``src/lunatp/interface.py:147-262``) for the UVU, UUU and UVW convolutions
+and the shared-weight UVW product.  The non-convolution uuu/uvu products of
+the reference are outside this library's scope and raise
+``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -61,6 +61,10 @@ def prepare_tensor_product(irreps_in1, irreps_in2=None, irreps_out=None, instruc
         _unsupported(inferred, False)
     if inferred == "uuu":
         return create_uuu_conv_operator(paths, dtype=dtype)
+    if inferred == "uvw":
+        from .uvw_conv import LunaTPUVWConv
+
+        return LunaTPUVWConv(paths, dtype=dtype)
     if inferred != "uvu":
         _unsupported(inferred, True)
     return create_uvu_conv_operator(paths, dtype=dtype)

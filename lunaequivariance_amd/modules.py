@@ -74,7 +74,7 @@ class TensorProductConv(torch.nn.Module):
 
     Pass irreps and instructions, an existing configuration (or e3nn-like
     module with the same attributes), or prebuilt metadata with ``mode="uvu"`` or
-    ``mode="uuu"``.
+    ``mode="uuu"``.  uvu, uuu and uvw instructions are supported.
     Build topology with ``create_graph`` and pass ``graph=`` on every call.
     """
 
@@ -117,10 +117,13 @@ class TensorProductConv(torch.nn.Module):
             weight = getattr(tp, "weight", None)
             if dtype is None:
                 dtype = weight.dtype if isinstance(weight, torch.Tensor) else torch.get_default_dtype()
-        if mode not in ("uvu", "uuu"):
-            raise NotImplementedError(f"{mode} convolution is not part of this MI355X build")
+        if metadata and mode not in ("uvu", "uuu"):
+            raise ValueError('Prebuilt metadata requires mode="uuu" or mode="uvu"')
+        from .uvw_conv import create_uvw_conv_operator
+
         self.mode = mode + "_conv"
-        self._factory = create_uuu_conv_operator if mode == "uuu" else create_uvu_conv_operator
+        self._factory = {"uuu": create_uuu_conv_operator, "uvu": create_uvu_conv_operator,
+                         "uvw": create_uvw_conv_operator}[mode]
         self.op = self._factory(tp, dtype=dtype)
         if metadata:
             self.weight_numel = tp["weight_numel"]
@@ -131,6 +134,11 @@ class TensorProductConv(torch.nn.Module):
             self.instructions = tp.instructions
             self.weight_numel = tp.weight_numel
             self.internal_weights, self.shared_weights = tp.internal_weights, tp.shared_weights
+
+    @property
+    def weight(self):
+        """The configuration's registered weight (internal weights) or its empty buffer."""
+        return self.tp.weight
 
     def _apply(self, fn, recurse=True):
         dtype = fn(torch.empty(0, dtype=self.op.compute_dtype)).dtype

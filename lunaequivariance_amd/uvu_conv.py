@@ -117,8 +117,10 @@ def spec_text(meta: dict, dtype: torch.dtype) -> str:
     specs = meta["generated_specs"]
     offsets, l0_dim = l0_feature_layout(specs)
     bits = 64 if dtype == torch.float64 else 32
-    parts = [f"LUNAUVU1 {bits} {meta['in1_dim']} {meta['in2_dim']} {meta['out_dim']} "
-             f"{meta['weight_numel']} {len(specs)} {l0_dim}"]
+    head = (f"{bits} {meta['in1_dim']} {meta['in2_dim']} {meta['out_dim']} "
+            f"{meta['weight_numel']} {len(specs)} {l0_dim}")
+    # A broadcast weight row (one row read by every edge) needs the LUNAUVU2 header.
+    parts = [f"LUNAUVU2 {head} 1" if meta.get("broadcast_weights") else f"LUNAUVU1 {head}"]
     for index, spec in enumerate(specs):
         terms = spec["terms"]
         head = (f"{spec['x_offset']} {spec['y_offset']} {spec['out_offset']} {spec['weight_offset']} "
@@ -252,7 +254,8 @@ def run_forward(op, x, y, w, graph, env=None, want_l0=False):
     N, E = graph.num_nodes, graph.num_edges
     if x.shape != (N, op.in1_dim):
         raise ValueError(f"x must have shape ({N}, {op.in1_dim}); got {tuple(x.shape)}")
-    if y.shape != (E, op.in2_dim) or w.shape != (E, op.weight_numel):
+    weight_rows = 1 if op.meta.get("broadcast_weights") else E
+    if y.shape != (E, op.in2_dim) or w.shape != (weight_rows, op.weight_numel):
         raise ValueError("edge_attr/weight rows must match the graph's edges")
     plan = op.plan
     factory = torch.zeros if plan.info.fwd_needs_zero else torch.empty
@@ -276,6 +279,8 @@ def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, T
     plan = op.plan
     need_x, need_y, need_w, need_env = needs
     need_env = need_env and env is not None
+    if need_w and op.meta.get("broadcast_weights"):
+        raise ValueError("a broadcast weight row has no per-edge gradient")
     gx = gy = gw = genv = None
     if need_x:
         gx = torch.empty((N, op.in1_dim), device=x.device, dtype=x.dtype)

@@ -1,0 +1,208 @@
+"""UVW tensor-product convolution as aggregation on the HIP UVU kernels plus per-path GEMMs.
+
+For a uvw path p (``src/lunatp/uvw_conv/``, e3nn's uvw connection) and an edge
+e = (s -> t):
+
+    msg_p[e, w, k] = sum_{u,v} Z_p[e, k, u, v] W_p[u, v, w],
+    Z_p[e, k, u, v] = pw * sum_{i,j} C_ijk x[s, u, i] y[e, v, j]
+
+and ``out[t] = sum_{e -> t} env[e] * msg[e]``.  With shared weights the sum
+over edges commutes with the contraction over (u, v):
+
+    out_p[t] = (sum_{e -> t} env[e] Z_p[e]) W_p = A_p[t] W_p
+
+so the per-edge work is the aggregation ``A`` alone, which is a UVU
+convolution whose weights are all one (a single broadcast weight row, never
+read per edge) and whose output keeps every edge channel v in its own block;
+it runs on the HIP UVU kernels.  The contraction with ``W_p`` then happens
+once per node instead of once per edge: a plain GEMM per path
+([N * d3, mul1 * mul2] x [mul1 * mul2, mul3]).  Per-edge weights cannot be
+moved out of the edge sum: the same kernels aggregate over a graph whose
+destinations are the edges themselves (``Z`` per edge), the per-edge
+contraction is a batched GEMM, and the messages are summed at destinations.
+
+Every piece is differentiable (the UVU autograd classes for the aggregation,
+torch for the GEMMs and the sum), so derivatives of every order follow.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .cg import sparse_terms
+from .graph import LunaTPGraph, make_graph
+from .layout import TensorProductPaths
+from .uvu_conv import LunaTPUVUConv, UVUConvForward
+
+
+class LunaTPUVWConv:
+    """Prepared UVW convolution (``src/lunatp/interface.py:370-408``)."""
+
+    mode = "uvw_conv"
+    index_mode = "uvw_conv"
+
+    def __init__(self, tp, *, dtype=None, index_bits=32):
+        paths = TensorProductPaths.from_tensor_product(tp)
+        dtype = getattr(paths, "dtype", torch.float32) if dtype is None else dtype
+        if dtype not in (torch.float32, torch.float64):
+            raise ValueError(f"UVW convolution requires float32 or float64, got {dtype}")
+        if index_bits != 32:
+            raise ValueError("only 32-bit graph indexing is supported")
+        self.tp = paths
+        self.compute_dtype = dtype
+        self.index_bits = index_bits
+        self.weight_mode = "shared" if paths.shared_weights else "external"
+        self.in1_dim, self.in2_dim, self.out_dim = paths.irreps_in1.dim, paths.irreps_in2.dim, paths.irreps_out.dim
+        self.weight_numel = paths.weight_numel
+        in_slices, edge_slices = paths.irreps_in1.slices(), paths.irreps_in2.slices()
+        out_slices = paths.irreps_out.slices()
+        self.paths = []
+        specs = []
+        a_off = w_off = 0
+        max_channels = 1
+        for ins in paths.instructions:
+            if ins.connection_mode != "uvw":
+                raise ValueError(f"Only connection_mode='uvw' is supported, got {ins.connection_mode!r}.")
+            if not ins.has_weight:
+                raise ValueError("uvw instructions require weights")
+            mul1, ir1 = paths.irreps_in1[ins.i_in1]
+            mul2, ir2 = paths.irreps_in2[ins.i_in2]
+            mul3, ir3 = paths.irreps_out[ins.i_out]
+            if mul1 * mul2 * mul3 == 0:
+                w_off += mul1 * mul2 * mul3
+                continue
+            d1, d2, d3 = ir1.dim, ir2.dim, ir3.dim
+            terms = sparse_terms(ir1.l, ir2.l, ir3.l, float(ins.path_weight))
+            if dtype == torch.float32:
+                terms = [(i, j, k, float(torch.tensor(c, dtype=torch.float32))) for i, j, k, c in terms]
+            self.paths.append(dict(a_off=a_off, w_off=w_off, out_off=out_slices[ins.i_out].start, i_out=ins.i_out,
+                                   mul1=mul1, mul2=mul2, mul3=mul3, d3=d3))
+            for v in range(mul2):
+                specs.append({
+                    "x_offset": in_slices[ins.i_in1].start,
+                    "y_offset": edge_slices[ins.i_in2].start + v * d2,
+                    "out_offset": a_off + v * mul1 * d3,
+                    "weight_offset": 0, "weight_stride": 1,
+                    "channels": mul1, "d1": d1, "d2": d2, "d3": d3,
+                    "l1": ir1.l, "l2": ir2.l, "l3": ir3.l, "terms": terms,
+                })
+            max_channels = max(max_channels, mul1)
+            a_off += mul2 * mul1 * d3
+            w_off += mul1 * mul2 * mul3
+        if w_off != self.weight_numel:
+            raise ValueError(f"lowered weight_numel={w_off}, configuration reports {self.weight_numel}.")
+        self.aggregate_dim = a_off
+        self.agg = None
+        if specs:
+            meta = {"in1_dim": self.in1_dim, "in2_dim": self.in2_dim, "out_dim": a_off,
+                    "weight_numel": max_channels, "max_channels": max_channels, "generated_specs": specs,
+                    "broadcast_weights": True}
+            self.agg = LunaTPUVUConv(meta, dtype=dtype)
+        self._ones = {}
+
+    def __getstate__(self):
+        state = dict(self.__dict__)
+        state["_ones"] = {}
+        return state
+
+    def _unit_weights(self, like):
+        key = (like.device, like.dtype)
+        if key not in self._ones:
+            self._ones[key] = torch.ones((1, self.agg.weight_numel), device=like.device, dtype=like.dtype)
+        return self._ones[key]
+
+    def _aggregate(self, x, y, env, graph):
+        """A[t] = sum_{e -> t} env[e] Z[e] on the HIP UVU kernels (differentiable)."""
+        ones = self._unit_weights(x)
+        if torch.compiler.is_compiling():
+            from . import ops
+
+            out, _ = torch.ops.lunaeq_amd.uvu_conv_forward(x, y, ones, env, ops.graph_tables(graph),
+                                                            graph.num_nodes, False, self.agg.torch_config)
+            return out
+        return UVUConvForward.apply(self.agg, graph, False, x, y, ones, env)
+
+    def _contract(self, values, weight, rows):
+        """sum over paths of values_p (x) W_p into the output layout; weight [w] or [rows, w]."""
+        per_row = weight.dim() == 2
+        blocks = {}
+        for p in self.paths:
+            m1, m2, m3, d3 = p["mul1"], p["mul2"], p["mul3"], p["d3"]
+            a = values[:, p["a_off"]: p["a_off"] + m2 * m1 * d3].reshape(rows, m2, m1, d3)
+            if per_row:
+                W = weight[:, p["w_off"]: p["w_off"] + m1 * m2 * m3].reshape(rows, m1, m2, m3)
+                piece = torch.einsum("nvuk,nuvw->nwk", a, W)
+            else:
+                W = weight[p["w_off"]: p["w_off"] + m1 * m2 * m3].reshape(m1, m2, m3)
+                piece = torch.einsum("nvuk,uvw->nwk", a, W)
+            piece = piece.reshape(rows, m3 * d3)
+            key = p["out_off"]
+            blocks[key] = piece if key not in blocks else blocks[key] + piece
+        pieces, at = [], 0
+        for start in sorted(blocks):
+            if start > at:
+                pieces.append(values.new_zeros((rows, start - at)))
+            pieces.append(blocks[start])
+            at = start + blocks[start].shape[1]
+        if at < self.out_dim:
+            pieces.append(values.new_zeros((rows, self.out_dim - at)))
+        return torch.cat(pieces, 1) if pieces else values.new_zeros((rows, self.out_dim))
+
+    def _edge_graph(self, graph):
+        """The graph whose destinations are the edges: node e receives edge e from src[e]."""
+        rows = max(graph.num_nodes, graph.num_edges)
+        key = ("uvw_edge_graph", rows)
+        if key not in graph._tables:
+            ids = torch.arange(graph.num_edges, device=graph.src.device, dtype=torch.int64)
+            graph._tables[key] = make_graph(graph.src.to(torch.int64), ids, rows)
+        return graph._tables[key]
+
+    def run(self, x, edge_attr, weight=None, *, graph: LunaTPGraph, env=None, return_l0_feat=False):
+        return lunatp_uvw_conv_func(self, x, edge_attr, weight, graph=graph, env=env,
+                                    return_l0_feat=return_l0_feat)
+
+
+def create_uvw_conv_operator(tp, *, dtype=None):
+    return LunaTPUVWConv(tp, dtype=dtype)
+
+
+def lunatp_uvw_conv_func(op, x, edge_attr, weight=None, *, graph: LunaTPGraph, env=None, return_l0_feat=False):
+    """UVW messages summed at destinations (``src/lunatp/uvw_conv/interface.py:190-245``).
+
+    x [num_nodes, in1_dim], edge_attr [num_edges, in2_dim]; weight is shared
+    [weight_numel] (or [1, weight_numel]) for a shared-weight configuration
+    and per-edge [num_edges, weight_numel] otherwise; env [num_edges] or
+    [num_edges, 1].
+    """
+    if return_l0_feat:
+        raise ValueError("return_l0_feat is not available for UVW convolution")
+    if weight is None:
+        raise ValueError("UVW convolution requires weights")
+    N, E = graph.num_nodes, graph.num_edges
+    if x.shape != (N, op.in1_dim) or edge_attr.shape != (E, op.in2_dim):
+        raise ValueError("x / edge_attr do not match the graph and the irreps")
+    x = x.contiguous()
+    edge_attr = edge_attr.contiguous()
+    if env is not None:
+        env = env.reshape(-1).contiguous()
+    if op.weight_mode == "shared":
+        if weight.shape not in ((op.weight_numel,), (1, op.weight_numel)):
+            raise ValueError(f"shared UVW weights must have shape ({op.weight_numel},)")
+        weight = weight.reshape(-1)
+    elif weight.shape != (E, op.weight_numel):
+        raise ValueError(f"per-edge UVW weights must have shape ({E}, {op.weight_numel})")
+    if op.agg is None:
+        return x.new_zeros((N, op.out_dim))
+    if op.weight_mode == "shared":
+        aggregated = op._aggregate(x, edge_attr, env, graph)
+        return op._contract(aggregated, weight, N)
+    edges = op._edge_graph(graph)
+    rows = edges.num_nodes
+    xs = x if rows == N else torch.nn.functional.pad(x, (0, 0, 0, rows - N))
+    per_edge = op._aggregate(xs, edge_attr, env, edges)[:E]
+    messages = op._contract(per_edge, weight.contiguous(), E)
+    dst = graph.dst.to(torch.int64)
+    return x.new_zeros((N, op.out_dim)).index_add(0, dst, messages)
+
+
+__all__ = ["LunaTPUVWConv", "create_uvw_conv_operator", "lunatp_uvw_conv_func"]

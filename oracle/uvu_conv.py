@@ -12,6 +12,12 @@ multiplicity ``m2``:
                                           y[e, i2][v, j] w[e, off + u*m2 + v]
     out[n] = sum_{e: dst_e = n} env_e * msg[e]
 
+For a uvw instruction every input pair (u, v) feeds every output channel w,
+``msg[e, io][w, k] = pw * sum C[i, j, k] x[src_e, i1][u, i] y[e, i2][v, j]
+W[e, off + (u*m2 + v)*mo + w]`` (e3nn's weight layout), with W the per-edge
+weights or the shared row repeated (the reference's UVW conv tests use the same
+oracle, ``tests/lunatp/test_uvw_conv.py:33-50``).
+
 For a uuu instruction (``docs/operators/tensor_product.md:100-106``; the
 reference's UUU conv tests use the same e3nn-then-``index_add`` oracle,
 ``tests/lunatp/test_uuu_conv.py:30-45``) the channels are matched instead of
@@ -107,8 +113,12 @@ def edge_messages(in1, in2, out, instructions, x_src, y, w, weights=None):
             wb = w[:, w_off: w_off + m1] if has_w else xb.new_ones((E, m1))
             piece = pw * torch.einsum("ijk,eui,euj,eu->euk", cg, xb, yb, wb).reshape(E, mo * d3)
             w_off += m1 if has_w else 0
+        elif mode == "uvw":
+            wb = w[:, w_off: w_off + m1 * m2 * mo].reshape(E, m1, m2, mo)
+            piece = pw * torch.einsum("ijk,eui,evj,euvw->ewk", cg, xb, yb, wb).reshape(E, mo * d3)
+            w_off += m1 * m2 * mo
         else:
-            raise ValueError("oracle covers uvu and uuu instructions")
+            raise ValueError("oracle covers uvu, uuu and uvw instructions")
         pieces.append((io, piece))
         msg = msg + torch.nn.functional.pad(piece, (o_off[io], out_dim - o_off[io] - mo * d3))
     return msg, pieces
@@ -147,23 +157,28 @@ def brute_force(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, 
             m2, l2, _ = in2[i2]
             _, l3, _ = out[io]
             cg = wigner_3j(l1, l2, l3)
-            # uvu: every (u, v) pair; uuu: the matched pairs (u, u) only.
-            pairs = [(u, v) for u in range(m1) for v in range(m2)] if mode == "uvu" else [(u, u) for u in range(m1)]
-            for u, v in pairs:
-                if mode == "uvu":
-                    weight = w[e, w_off + u * m2 + v]
-                else:
-                    weight = w[e, w_off + u] if has_w else 1.0
+            mo = out[io][0]
+            # (u, v, output channel, weight index): uvu keeps u and mixes v;
+            # uuu matches u = v; uvw mixes both into every output channel.
+            if mode == "uvu":
+                quads = [(u, v, u, w_off + u * m2 + v) for u in range(m1) for v in range(m2)]
+            elif mode == "uuu":
+                quads = [(u, u, u, w_off + u if has_w else None) for u in range(m1)]
+            else:
+                quads = [(u, v, o, w_off + (u * m2 + v) * mo + o)
+                         for u in range(m1) for v in range(m2) for o in range(mo)]
+            for u, v, o, windex in quads:
+                weight = 1.0 if windex is None else w[e, windex]
                 for i in range(2 * l1 + 1):
                     for j in range(2 * l2 + 1):
                         for k in range(2 * l3 + 1):
                             c = cg[i, j, k]
                             if c == 0.0:
                                 continue
-                            result[dst[e], o_off[io] + u * (2 * l3 + 1) + k] += (
+                            result[dst[e], o_off[io] + o * (2 * l3 + 1) + k] += (
                                 pw * c * x[src[e], x_off[i1] + u * (2 * l1 + 1) + i]
                                 * y[e, y_off[i2] + v * (2 * l2 + 1) + j] * weight)
-            w_off += m1 * m2 if mode == "uvu" else (m1 if has_w else 0)
+            w_off += {"uvu": m1 * m2, "uuu": m1 if has_w else 0, "uvw": m1 * m2 * mo}[mode]
     return result
 
 
