@@ -40,6 +40,11 @@ CONFIGS = {
     "uuu_l2": dict(channels=64, atoms=2083, lmax=2, dtype="float32"),
     "uuu_l3": dict(channels=64, atoms=2083, lmax=3, dtype="float32"),
     "uuu_l4": dict(channels=64, atoms=2083, lmax=4, dtype="float32"),
+    # UVW conv (docs/operators/tensor_product_conv.md:266-292): the same graph, 64 channels
+    # per degree, edge features = one spherical-harmonic channel per degree, shared weights.
+    "uvw_l2": dict(channels=64, atoms=2083, lmax=2, dtype="float32", mode="uvw"),
+    "uvw_l3": dict(channels=64, atoms=2083, lmax=3, dtype="float32", mode="uvw"),
+    "uvw_l4": dict(channels=64, atoms=2083, lmax=4, dtype="float32", mode="uvw"),
 }
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
@@ -87,7 +92,7 @@ def main():
     if args.config == "cfg5":
         bench_uvw(args)
         return
-    if args.config.startswith("uuu"):
+    if args.config.startswith(("uuu", "uvw_")):
         bench_uuu(args)
         return
 
@@ -283,7 +288,7 @@ def bench_uuu(args):
 
     import lunaequivariance_amd as lunaeq
     from lunaequivariance_amd import _native
-    from lunaequivariance_amd.workloads import periodic_radius_graph
+    from lunaequivariance_amd.workloads import periodic_radius_graph, spherical_harmonics
 
     cfg = CONFIGS[args.config]
     dtype = getattr(torch, cfg["dtype"])
@@ -291,19 +296,28 @@ def bench_uuu(args):
     device = torch.device("cuda:0")
     torch.manual_seed(0)
     ch, lmax, N = cfg["channels"], cfg["lmax"], cfg["atoms"]
-    ir = "+".join(f"{ch}x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(lmax + 1))
-    a = lunaeq.Irreps(ir)
-    instructions = [(i, j, k, "uuu", True) for i, (_, p) in enumerate(a) for j, (_, q) in enumerate(a)
+    mode = cfg.get("mode", "uuu")
+    parity = lambda l: "e" if l % 2 == 0 else "o"  # noqa: E731
+    ir = "+".join(f"{ch}x{l}{parity(l)}" for l in range(lmax + 1))
+    edge_ir = ir if mode == "uuu" else "+".join(f"1x{l}{parity(l)}" for l in range(lmax + 1))
+    a, b = lunaeq.Irreps(ir), lunaeq.Irreps(edge_ir)
+    instructions = [(i, j, k, mode, True) for i, (_, p) in enumerate(a) for j, (_, q) in enumerate(b)
                     for k, (_, r) in enumerate(a) if r in p * q]
-    conv = lunaeq.TensorProductConv(ir, ir, ir, instructions, internal_weights=False, shared_weights=False,
-                                    dtype=dtype)
+    conv = lunaeq.TensorProductConv(ir, edge_ir, ir, instructions, internal_weights=False,
+                                    shared_weights=mode == "uvw", dtype=dtype)
     # density 0.0787 atoms/A^3 and a 5 A cutoff give ~41 neighbours per atom
-    src, dst, *_ = periodic_radius_graph(N, 0.0787, 5.0, seed=0, device=device)
+    src, dst, _pos, vec, _box = periodic_radius_graph(N, 0.0787, 5.0, seed=0, device=device)
     E = src.numel()
     graph = conv.create_graph(src, dst, N)
     x = torch.randn(N, a.dim, device=device, dtype=dtype, requires_grad=True)
-    y = torch.randn(E, a.dim, device=device, dtype=dtype, requires_grad=True)
-    w = (torch.randn(E, conv.weight_numel, device=device, dtype=dtype) / len(instructions) ** 0.5).requires_grad_()
+    if mode == "uuu":
+        y = torch.randn(E, a.dim, device=device, dtype=dtype, requires_grad=True)
+        w = (torch.randn(E, conv.weight_numel, device=device, dtype=dtype) / len(instructions) ** 0.5)
+    else:
+        y = spherical_harmonics(lmax, vec).to(dtype).requires_grad_()
+        w = torch.randn(conv.weight_numel, device=device, dtype=dtype) / len(instructions) ** 0.5
+    w.requires_grad_()
+    del vec
     g = torch.randn(N, a.dim, device=device, dtype=dtype)
 
     def forward():
@@ -343,7 +357,12 @@ def bench_uuu(args):
     if not args.step_only:
         ms_fwd, _ = timed(forward, args.steps)
         ms_force, _ = timed(force_step, max(1, args.steps // 2))
-    algo = uuu_algorithmic_bytes(N, E, a.dim, a.dim, a.dim, conv.weight_numel, real)
+    if mode == "uuu":
+        algo = uuu_algorithmic_bytes(N, E, a.dim, a.dim, a.dim, conv.weight_numel, real)
+    else:
+        # The aggregation runs on the UVU kernels with a broadcast weight row (no weight traffic)
+        # into A [N, aggregate_dim]; the per-path GEMMs are library calls.
+        algo = algorithmic_bytes(N, E, a.dim, b.dim, conv.op.aggregate_dim, 0, real)
     per_kernel = {}
     for name, (count, total, low, high) in kernels.items():
         avg = total / count
@@ -354,19 +373,25 @@ def bench_uuu(args):
             entry["gbs"] = round(algo[name] / (total / args.steps / 1000.0) / 1e9, 1)
             entry["launches_per_step"] = launches_per_step
         per_kernel[name] = entry
-    dominant = max(algo, key=lambda n: kernels.get(n, (0, 0))[1])
+    dominant = max((n for n in algo if n in kernels), key=lambda n: kernels[n][1])
     achieved = per_kernel[dominant]["gbs"]
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(ir, ir, ir, instructions, x, y, w, g, src, dst, N, 40, dtype)
+        wcpu = w if mode == "uuu" else w.detach().reshape(1, -1).expand(E, -1)
+        cpu = cpu_baseline(ir, edge_ir, ir, instructions, x, y, wcpu, g, src, dst, N, 40, dtype)
+        # in the metric's unit: the sample's edges/s times the graph's atoms per edge
+        cpu["value"] = round(cpu["value"] * N / E, 1)
+        cpu["unit"] = "atoms/s"
+        cpu["sample"] += f"; edges/s scaled by atoms/edges = {N}/{E}"
     print(json.dumps({
-        "metric": "UUU TP-conv atoms/s fwd+bwd", "value": round(N / (ms_step / 1000.0), 1), "unit": "atoms/s",
+        "metric": f"{mode.upper()} TP-conv atoms/s fwd+bwd", "value": round(N / (ms_step / 1000.0), 1), "unit": "atoms/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32" if dtype == torch.float32 else "f64",
         "data": "synthetic (periodic random atoms, radius graph, random features and per-edge weights)",
-        "config": {"workload": f"{args.config}: UUU conv, {ch} channels per degree, lmax={lmax}, every uuu path, "
-                               f"{N} atoms, {E} edges, per-edge weights, fwd+bwd",
+        "config": {"workload": f"{args.config}: {mode.upper()} conv, {ch} channels per degree, lmax={lmax}, "
+                               f"every {mode} path, edge irreps {edge_ir}, {N} atoms, {E} edges, "
+                               f"{'per-edge' if mode == 'uuu' else 'shared'} weights, fwd+bwd",
                    "num_nodes": N, "num_edges": E, "weight_numel": conv.weight_numel,
                    "paths": len(instructions), "parallelism": "single GPU"},
         "forward_atoms_per_s": round(N / (ms_fwd / 1000.0), 1),

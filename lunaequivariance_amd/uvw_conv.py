@@ -15,8 +15,10 @@ so the per-edge work is the aggregation ``A`` alone, which is a UVU
 convolution whose weights are all one (a single broadcast weight row, never
 read per edge) and whose output keeps every edge channel v in its own block;
 it runs on the HIP UVU kernels.  The contraction with ``W_p`` then happens
-once per node instead of once per edge: a plain GEMM per path
-([N * d3, mul1 * mul2] x [mul1 * mul2, mul3]).  Per-edge weights cannot be
+once per node instead of once per edge: the paths into one output block are
+contiguous columns of A, so each output block is one batched library GEMM
+(``W_o^T [mul3, C] @ A_o [N, C, d3]``, C = the sum of mul1 * mul2 over its
+paths), which lands directly in the output layout.  Per-edge weights cannot be
 moved out of the edge sum: the same kernels aggregate over a graph whose
 destinations are the edges themselves (``Z`` per edge), the per-edge
 contraction is a batched GEMM, and the messages are summed at destinations.
@@ -26,6 +28,8 @@ torch for the GEMMs and the sum), so derivatives of every order follow.
 """
 
 from __future__ import annotations
+
+from math import prod
 
 import torch
 
@@ -60,7 +64,17 @@ class LunaTPUVWConv:
         specs = []
         a_off = w_off = 0
         max_channels = 1
+        # Aggregate blocks in output order, so the paths into one output block are
+        # contiguous columns of A and contract in one GEMM.
+        w_offsets, at = [], 0
         for ins in paths.instructions:
+            w_offsets.append(at)
+            at += prod(ins.path_shape) if ins.has_weight else 0
+        order = sorted(range(len(paths.instructions)),
+                       key=lambda n: out_slices[paths.instructions[n].i_out].start)
+        for n in order:
+            ins = paths.instructions[n]
+            w_off = w_offsets[n]
             if ins.connection_mode != "uvw":
                 raise ValueError(f"Only connection_mode='uvw' is supported, got {ins.connection_mode!r}.")
             if not ins.has_weight:
@@ -69,7 +83,6 @@ class LunaTPUVWConv:
             mul2, ir2 = paths.irreps_in2[ins.i_in2]
             mul3, ir3 = paths.irreps_out[ins.i_out]
             if mul1 * mul2 * mul3 == 0:
-                w_off += mul1 * mul2 * mul3
                 continue
             d1, d2, d3 = ir1.dim, ir2.dim, ir3.dim
             terms = sparse_terms(ir1.l, ir2.l, ir3.l, float(ins.path_weight))
@@ -88,9 +101,24 @@ class LunaTPUVWConv:
                 })
             max_channels = max(max_channels, mul1)
             a_off += mul2 * mul1 * d3
-            w_off += mul1 * mul2 * mul3
-        if w_off != self.weight_numel:
-            raise ValueError(f"lowered weight_numel={w_off}, configuration reports {self.weight_numel}.")
+        if at != self.weight_numel:
+            raise ValueError(f"lowered weight_numel={at}, configuration reports {self.weight_numel}.")
+        # Per output block: its columns of A as [C = sum of mul2 * mul1, d3] and the
+        # weight rows in the same (path, v, u) order, gathered by one index.
+        self.blocks, perm = [], []
+        for p in self.paths:
+            m1, m2, m3 = p["mul1"], p["mul2"], p["mul3"]
+            if not self.blocks or self.blocks[-1]["out_off"] != p["out_off"]:
+                self.blocks.append(dict(out_off=p["out_off"], d3=p["d3"], mul3=m3, a_lo=p["a_off"], channels=0,
+                                        w_lo=len(perm)))
+            block = self.blocks[-1]
+            block["channels"] += m2 * m1
+            for v in range(m2):
+                for u in range(m1):
+                    for w in range(m3):
+                        perm.append(p["w_off"] + (u * m2 + v) * m3 + w)
+        self._perm = torch.tensor(perm, dtype=torch.int64)
+        self._perm_cache = {}
         self.aggregate_dim = a_off
         self.agg = None
         if specs:
@@ -103,6 +131,7 @@ class LunaTPUVWConv:
     def __getstate__(self):
         state = dict(self.__dict__)
         state["_ones"] = {}
+        state["_perm_cache"] = {}
         return state
 
     def _unit_weights(self, like):
@@ -123,30 +152,27 @@ class LunaTPUVWConv:
         return UVUConvForward.apply(self.agg, graph, False, x, y, ones, env)
 
     def _contract(self, values, weight, rows):
-        """sum over paths of values_p (x) W_p into the output layout; weight [w] or [rows, w]."""
+        """out[n, o + w*d3 + k] = sum_c W[c, w] A[n, c, k] per output block (one batched GEMM
+        each); weight is the shared row [weight_numel] or per-row [rows, weight_numel]."""
+        key = weight.device
+        if key not in self._perm_cache:
+            self._perm_cache[key] = self._perm.to(weight.device)
+        perm = self._perm_cache[key]
         per_row = weight.dim() == 2
-        blocks = {}
-        for p in self.paths:
-            m1, m2, m3, d3 = p["mul1"], p["mul2"], p["mul3"], p["d3"]
-            a = values[:, p["a_off"]: p["a_off"] + m2 * m1 * d3].reshape(rows, m2, m1, d3)
-            if per_row:
-                W = weight[:, p["w_off"]: p["w_off"] + m1 * m2 * m3].reshape(rows, m1, m2, m3)
-                piece = torch.einsum("nvuk,nuvw->nwk", a, W)
-            else:
-                W = weight[p["w_off"]: p["w_off"] + m1 * m2 * m3].reshape(m1, m2, m3)
-                piece = torch.einsum("nvuk,uvw->nwk", a, W)
-            piece = piece.reshape(rows, m3 * d3)
-            key = p["out_off"]
-            blocks[key] = piece if key not in blocks else blocks[key] + piece
+        gathered = weight.index_select(-1, perm)
         pieces, at = [], 0
-        for start in sorted(blocks):
-            if start > at:
-                pieces.append(values.new_zeros((rows, start - at)))
-            pieces.append(blocks[start])
-            at = start + blocks[start].shape[1]
+        for blk in self.blocks:
+            C, d3, m3 = blk["channels"], blk["d3"], blk["mul3"]
+            a = values[:, blk["a_lo"]: blk["a_lo"] + C * d3].reshape(rows, C, d3)
+            W = gathered[..., blk["w_lo"]: blk["w_lo"] + C * m3]
+            Wt = W.reshape(rows, C, m3).transpose(1, 2) if per_row else W.reshape(C, m3).t()
+            if blk["out_off"] > at:
+                pieces.append(values.new_zeros((rows, blk["out_off"] - at)))
+            pieces.append(torch.matmul(Wt, a).reshape(rows, m3 * d3))
+            at = blk["out_off"] + m3 * d3
         if at < self.out_dim:
             pieces.append(values.new_zeros((rows, self.out_dim - at)))
-        return torch.cat(pieces, 1) if pieces else values.new_zeros((rows, self.out_dim))
+        return torch.cat(pieces, 1) if len(pieces) > 1 else pieces[0]
 
     def _edge_graph(self, graph):
         """The graph whose destinations are the edges: node e receives edge e from src[e]."""
