@@ -39,6 +39,44 @@ from .layout import TensorProductPaths
 from .uvu_conv import LunaTPUVUConv, UVUConvForward
 
 
+def _split_k_tn(a, b, chunks=16):
+    """a^T @ b for tall a [K, M], b [K, N] as `chunks` partial GEMMs and a sum: the
+    library GEMM on a long K and a small M x N output leaves most of the chip idle.
+    The last K % chunks rows join with one more small GEMM (no padded copies)."""
+    K = a.shape[0]
+    if K < 4096:
+        return a.t() @ b
+    step = K // chunks
+    main = step * chunks
+    out = torch.bmm(a[:main].reshape(chunks, step, -1).transpose(1, 2), b[:main].reshape(chunks, step, -1)).sum(0)
+    if main < K:
+        out = torch.addmm(out, a[main:].t(), b[main:])
+    return out
+
+
+class _RowsTimesWeight(torch.autograd.Function):
+    """rows [K, C] @ W [C, M] whose weight gradient is a split-K GEMM.  The backward is
+    written in differentiable operations, so higher derivatives compose."""
+
+    @staticmethod
+    def forward(ctx, rows, weight):
+        ctx.save_for_backward(rows, weight)
+        return rows @ weight
+
+    @staticmethod
+    def backward(ctx, grad):
+        rows, weight = ctx.saved_tensors
+        grad_rows = grad @ weight.t() if ctx.needs_input_grad[0] else None
+        grad_weight = _split_k_tn(rows, grad) if ctx.needs_input_grad[1] else None
+        return grad_rows, grad_weight
+
+
+def _rows_times_weight(rows, weight):
+    if torch.compiler.is_compiling():
+        return rows @ weight
+    return _RowsTimesWeight.apply(rows, weight)
+
+
 class LunaTPUVWConv:
     """Prepared UVW convolution (``src/lunatp/interface.py:370-408``)."""
 
@@ -152,23 +190,33 @@ class LunaTPUVWConv:
         return UVUConvForward.apply(self.agg, graph, False, x, y, ones, env)
 
     def _contract(self, values, weight, rows):
-        """out[n, o + w*d3 + k] = sum_c W[c, w] A[n, c, k] per output block (one batched GEMM
-        each); weight is the shared row [weight_numel] or per-row [rows, weight_numel]."""
+        """out[n, o + w*d3 + k] = sum_c W[c, w] A[n, c, k] per output block; weight is the
+        shared row [weight_numel] or per-row [rows, weight_numel].
+
+        Shared weights: one 2-D GEMM per block over rows (n, k), [rows * d3, C] x [C, mul3],
+        so the weight gradient is also one GEMM.  Per-row weights: a batched GEMM.  The
+        blocks are taken with one split (its backward is one concatenation).
+        """
         key = weight.device
         if key not in self._perm_cache:
             self._perm_cache[key] = self._perm.to(weight.device)
-        perm = self._perm_cache[key]
         per_row = weight.dim() == 2
-        gathered = weight.index_select(-1, perm)
+        gathered = weight.index_select(-1, self._perm_cache[key])
+        a_blocks = values.split([blk["channels"] * blk["d3"] for blk in self.blocks], 1)
+        w_blocks = gathered.split([blk["channels"] * blk["mul3"] for blk in self.blocks], -1)
         pieces, at = [], 0
-        for blk in self.blocks:
+        for blk, a, W in zip(self.blocks, a_blocks, w_blocks):
             C, d3, m3 = blk["channels"], blk["d3"], blk["mul3"]
-            a = values[:, blk["a_lo"]: blk["a_lo"] + C * d3].reshape(rows, C, d3)
-            W = gathered[..., blk["w_lo"]: blk["w_lo"] + C * m3]
-            Wt = W.reshape(rows, C, m3).transpose(1, 2) if per_row else W.reshape(C, m3).t()
+            if per_row:
+                piece = torch.matmul(W.reshape(rows, C, m3).transpose(1, 2), a.reshape(rows, C, d3))
+            elif d3 == 1:
+                piece = _rows_times_weight(a, W.reshape(C, m3))
+            else:
+                rows_k = a.reshape(rows, C, d3).transpose(1, 2).reshape(rows * d3, C)
+                piece = _rows_times_weight(rows_k, W.reshape(C, m3)).reshape(rows, d3, m3).transpose(1, 2)
             if blk["out_off"] > at:
                 pieces.append(values.new_zeros((rows, blk["out_off"] - at)))
-            pieces.append(torch.matmul(Wt, a).reshape(rows, m3 * d3))
+            pieces.append(piece.reshape(rows, m3 * d3))
             at = blk["out_off"] + m3 * d3
         if at < self.out_dim:
             pieces.append(values.new_zeros((rows, self.out_dim - at)))
