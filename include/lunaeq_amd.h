@@ -74,6 +74,12 @@ int luna_device_count(void);
  *   "<x_off> <y_off> <out_off> <w_off> <w_stride> <channels> <d1> <d2> <d3>
  *    <l0_col or -1> <nterms> (<i> <j> <k> <coefficient>)*nterms"
  *
+ * The header "LUNAUVU2 <dtype_bits> <in1> <in2> <out> <weight_numel> <npaths>
+ * <l0_dim> <w_broadcast>" is the same with one flag: when w_broadcast is 1 the
+ * weight operand w is a single row [1, weight_numel] read by every edge (no
+ * per-edge weight traffic; gw must then be NULL in luna_uvu_conv_bwd).  The
+ * UVW convolution uses it with a row of ones to aggregate per-node sums of the
+ * edge products before its weight contraction.
  * Coefficients already include the path weight.  Kernels are emitted and
  * compiled here (or loaded from the code-object cache in cache_dir, which may
  * be NULL for no cache); loading onto a device is deferred to first launch.
