@@ -727,16 +727,17 @@ unsigned blocks_for(int64_t items) {
   return (unsigned)items;
 }
 
-// Waves per workgroup sharing one node's edges: enough workgroups times waves
-// to give every SIMD of the chip about eight waves, at most 8 per node.
-int split_for(int64_t workgroups) {
-  int split = 1;
-  while (split < 8 && workgroups * split < 8192) split *= 2;
-  return split;
-}
-
 size_t lds_bytes(int split, int accumulators, int bits) {
   return split > 1 ? (size_t)(split / 2) * accumulators * 64 * (bits / 8) : 0;
+}
+
+// Waves per workgroup sharing one node's edges: enough workgroups times waves
+// to give every SIMD of the chip about eight waves, at most 8 per node, and
+// no more than 64 KiB of LDS for the partial sums.
+int split_for(int64_t workgroups, int accumulators, int bits) {
+  int split = 1;
+  while (split < 8 && workgroups * split < 8192 && lds_bytes(split * 2, accumulators, bits) <= 65536) split *= 2;
+  return split;
 }
 
 }  // namespace
@@ -824,9 +825,9 @@ int luna_uuu_conv_fwd(const LunaUuuPlan* cplan, const void* x, const void* y, co
     for (size_t gi = 0; gi < p.fwd.size(); ++gi) {
       const UGroup& g = p.fwd[gi];
       const int64_t items = num_nodes * g.chunks;
-      int split = split_for(items);
       int accs = 0;
       for (int b : g.obs) accs += p.spec.oblocks[b].d;
+      int split = split_for(items, accs, p.spec.bits);
       void* args[] = {&x, &y, &w, &env, &src, &dst_rowptr, &node_order, &out, &l0, &split};
       launch("uuu_fwd", function_for(module, "luna_uuu_fwd_g" + std::to_string(gi)), dim3(blocks_for(items)),
              dim3(64 * split), (hipStream_t)stream, args, (unsigned)lds_bytes(split, accs, p.spec.bits));
@@ -880,10 +881,10 @@ int luna_uuu_conv_bwd(const LunaUuuPlan* cplan, const void* x, const void* y, co
     for (size_t gi = 0; gi < p.bwd.size(); ++gi) {
       const UGroup& grp = p.bwd[gi];
       const int64_t items = num_nodes * grp.chunks;
-      int split = split_for(items);
       int accs = 0;
       if (gx)
         for (int b : grp.xbs) accs += p.spec.xblocks[b].d;
+      int split = split_for(items, accs, p.spec.bits);
       void* args[] = {&x, &y, &w, &env, &g, &gl0, &dst, &src_rowptr, &edge_ids_by_src, &source_node_order,
                       &gx, &gy, &gw, &part, &split, &E};
       launch("uuu_bwd", function_for(module, "luna_uuu_bwd_g" + std::to_string(gi)), dim3(blocks_for(items)),
