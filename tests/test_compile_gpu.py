@@ -74,3 +74,53 @@ def test_dispatcher_ops_differentiate_to_second_order():
     second_e = torch.autograd.grad(first_e, (x, y, w), dirs)
     for a, b in zip(second_o, second_e):
         assert_close(a, b.double(), torch.float32, "op second order")
+
+
+def other_mode_problem(mode, seed=0, nodes=10, edges=40):
+    ir = "8x0e+8x1o+8x2e"
+    edge = ir if mode == "uuu" else "1x0e+1x1o+1x2e"
+    a, b = lunaeq.Irreps(ir), lunaeq.Irreps(edge)
+    instructions = [(i, j, k, mode, True) for i, (m, p) in enumerate(a) for j, (n, q) in enumerate(b)
+                    for k, (o, r) in enumerate(a) if r in p * q and (mode != "uuu" or m == n == o)]
+    conv = lunaeq.TensorProductConv(ir, edge, ir, instructions, internal_weights=False,
+                                    shared_weights=mode == "uvw")
+    gen = torch.Generator().manual_seed(seed)
+    src = torch.randint(nodes, (edges,), generator=gen)
+    dst = torch.sort(torch.randint(nodes, (edges,), generator=gen))[0]
+    graph = conv.create_graph(src.to(DEV), dst.to(DEV), nodes)
+    x = torch.randn(nodes, a.dim, generator=gen).to(DEV).requires_grad_()
+    y = torch.randn(edges, b.dim, generator=gen).to(DEV).requires_grad_()
+    wshape = (conv.weight_numel,) if mode == "uvw" else (edges, conv.weight_numel)
+    w = torch.randn(wshape, generator=gen).to(DEV).requires_grad_()
+    return conv, graph, x, y, w
+
+
+@pytest.mark.parametrize("mode", ["uuu", "uvw"])
+def test_compiled_uuu_and_uvw_match_eager(mode):
+    """UUU runs through lunaeq_amd::uuu_conv_*, the shared-weight UVW aggregation through
+    lunaeq_amd::uvu_conv_* plus library GEMMs; compiled forward and first order equal eager."""
+    conv, graph, x, y, w = other_mode_problem(mode)
+
+    def layer(a, b, c):
+        return conv(a, b, c, graph=graph)
+
+    torch._dynamo.reset()
+    compiled = torch.compile(layer, backend="aot_eager", fullgraph=True)
+    eager_out = layer(x, y, w)
+    out = compiled(x, y, w)
+    assert_close(out, eager_out.double(), torch.float32, f"{mode} compiled forward")
+    seed = torch.randn_like(out)
+    for a, b in zip(torch.autograd.grad(out, (x, y, w), seed), torch.autograd.grad(eager_out, (x, y, w), seed)):
+        assert_close(a, b.double(), torch.float32, f"{mode} compiled first order")
+
+
+def test_opcheck_uuu():
+    conv, graph, x, y, w = other_mode_problem("uuu", seed=2)
+    tables = ops.graph_tables(graph)
+    config = conv.op.torch_config
+    torch.library.opcheck(torch.ops.lunaeq_amd.uuu_conv_forward.default,
+                          (x, y, w, None, tables, graph.num_nodes, False, config))
+    g = torch.randn(graph.num_nodes, conv.irreps_out.dim, device=DEV)
+    torch.library.opcheck(torch.ops.lunaeq_amd.uuu_conv_backward.default,
+                          (x.detach(), y.detach(), w.detach(), None, g, None, tables, graph.num_nodes,
+                           [True, True, True, False], config))
