@@ -124,3 +124,32 @@ def test_opcheck_uuu():
     torch.library.opcheck(torch.ops.lunaeq_amd.uuu_conv_backward.default,
                           (x.detach(), y.detach(), w.detach(), None, g, None, tables, graph.num_nodes,
                            [True, True, True, False], config))
+
+
+def test_uuu_dispatcher_ops_second_order_with_unweighted_paths():
+    """The dispatcher ops' double backward substitutes weight directions through the
+    weight-linear operator (unweighted paths make the product affine in w)."""
+    ir = "8x0e+8x1o"
+    a = lunaeq.Irreps(ir)
+    paths = [(i, j, k, "uuu", n % 2 == 0)
+             for n, (i, j, k) in enumerate((i, j, k) for i, (_, p) in enumerate(a) for j, (_, q) in enumerate(a)
+                                          for k, (_, r) in enumerate(a) if r in p * q)]
+    conv = lunaeq.TensorProductConv(ir, ir, ir, paths, internal_weights=False, shared_weights=False)
+    gen = torch.Generator().manual_seed(5)
+    nodes, edges = 9, 30
+    src = torch.randint(nodes, (edges,), generator=gen)
+    dst = torch.sort(torch.randint(nodes, (edges,), generator=gen))[0]
+    graph = conv.create_graph(src.to(DEV), dst.to(DEV), nodes)
+    x = torch.randn(nodes, a.dim, generator=gen).to(DEV).requires_grad_()
+    y = torch.randn(edges, a.dim, generator=gen).to(DEV).requires_grad_()
+    w = torch.randn(edges, conv.weight_numel, generator=gen).to(DEV).requires_grad_()
+    out, _ = torch.ops.lunaeq_amd.uuu_conv_forward(x, y, w, None, ops.graph_tables(graph), nodes, False,
+                                                   conv.op.torch_config)
+    eager = conv(x, y, w, graph=graph)
+    assert_close(out, eager.double(), torch.float32, "uuu op forward")
+    seed = torch.randn_like(out)
+    first_o = torch.autograd.grad(out, (x, y, w), seed, create_graph=True)
+    first_e = torch.autograd.grad(eager, (x, y, w), seed, create_graph=True)
+    dirs = [torch.randn_like(t) for t in first_e]
+    for a_, b_ in zip(torch.autograd.grad(first_o, (x, y, w), dirs), torch.autograd.grad(first_e, (x, y, w), dirs)):
+        assert_close(a_, b_.double(), torch.float32, "uuu op second order")
