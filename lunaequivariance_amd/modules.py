@@ -16,8 +16,10 @@ from .uvu_conv import create_uvu_conv_operator
 class TensorProduct(torch.nn.Module):
     """Row-wise tensor product (``src/modules/tensorproduct.py:19-116``).
 
-    This build provides the shared-weight ``uvw`` connection on matrix cores
-    (fp32); weights are the configuration's registered parameter unless given.
+    This build provides the ``uvw`` connection: shared weights in fp32 on
+    matrix-core kernels, fp64 and per-row weights through the row form of the
+    UVW convolution.  Weights are the configuration's registered parameter
+    unless given.
     """
 
     def __init__(self, irreps_in1, irreps_in2=None, irreps_out=None, instructions=None,
@@ -62,6 +64,15 @@ class TensorProduct(torch.nn.Module):
     @property
     def weight(self):
         return self.tp.weight
+
+    def _apply(self, fn, recurse=True):
+        from .uvw import LunaTPUVW
+
+        dtype = fn(torch.empty(0, dtype=self.op.compute_dtype)).dtype
+        result = super()._apply(fn, recurse=recurse)
+        if dtype in (torch.float32, torch.float64) and dtype != self.op.compute_dtype:
+            self.op = LunaTPUVW(self.tp, dtype=dtype)
+        return result
 
     def forward(self, x, y, weight=None):
         if weight is None and self.internal_weights:

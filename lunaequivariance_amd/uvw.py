@@ -1,4 +1,5 @@
-"""Shared-weight UVW tensor product (matrix-core kernels, fp32).
+"""UVW tensor product: shared-weight matrix-core kernels in fp32, and the row form
+of the UVW convolution for fp64 and per-row weights.
 
 ``out[b, io][w, k] = sum_paths pw * sum_{u,v} W[u, v, w] sum_{ij} c_ijk x[b, i1][u, i] y[b, i2][v, j]``
 with one weight tensor shared by every row (e3nn ``connection_mode="uvw"``,
@@ -7,6 +8,11 @@ with one weight tensor shared by every row (e3nn ``connection_mode="uvw"``,
 forward and two backward kernels whose contractions over ``(u, v)`` and over
 rows run on ``v_mfma_f32_32x32x2f32``.  Autograd composes higher orders from
 the forward and backward kernels, as for the convolution.
+
+fp64 and per-row weights (``shared_weights=False``) take the UVW convolution
+over the identity graph (row b is node b and edge b): the CG products of each
+row on the HIP UVU kernels, the weight contraction as library GEMMs (on the
+fp64 matrix cores for fp64).
 """
 
 from __future__ import annotations
@@ -93,15 +99,23 @@ class LunaTPUVW:
         tp = TensorProductPaths.from_tensor_product(tp)
         self.tp = tp
         self.compute_dtype = getattr(tp, "dtype", torch.float32) if dtype is None else dtype
-        if self.compute_dtype != torch.float32:
-            raise NotImplementedError("the matrix-core UVW tensor product runs in float32")
+        if self.compute_dtype not in (torch.float32, torch.float64):
+            raise ValueError(f"UVW requires float32 or float64, got {self.compute_dtype}")
         self.meta = build_uvw_metadata(tp, self.compute_dtype)
         self.weight_mode = self.meta["weight_mode"]
-        if self.weight_mode != "shared":
-            raise NotImplementedError("UVW with per-row weights is not part of this build")
         self.out_dim = self.meta["out_dim"]
-        self.spec = uvw_spec_text(self.meta)
         self._plan = None
+        self._identity = {}
+        # fp32 with shared weights: the matrix-core kernels; otherwise the row form
+        # of the convolution.
+        self.rows_op = None
+        if self.compute_dtype != torch.float32 or self.weight_mode != "shared":
+            from .uvw_conv import LunaTPUVWConv
+
+            self.rows_op = LunaTPUVWConv(tp, dtype=self.compute_dtype)
+            self.spec = None
+        else:
+            self.spec = uvw_spec_text(self.meta)
 
     @property
     def plan(self) -> NativeUvwPlan:
@@ -110,7 +124,37 @@ class LunaTPUVW:
         return self._plan
 
     def run(self, x, y, weight):
+        if self.rows_op is not None:
+            return self._run_rows(x, y, weight)
         return lunatp_uvw_func(self, x, y, weight)
+
+    def identity_graph(self, rows, device):
+        """Row b is node b and edge b (cached per size and device)."""
+        key = (rows, str(device))
+        if key not in self._identity:
+            from .graph import make_graph
+
+            ids = torch.arange(rows, device=device)
+            graph = make_graph(ids, ids, rows)
+            graph._tables["identity"] = True
+            self._identity = {key: graph}
+        return self._identity[key]
+
+    def _run_rows(self, x, y, weight):
+        if weight is None:
+            raise TypeError("UVW requires a weight tensor")
+        if x.ndim != 2 or y.ndim != 2 or y.shape[0] != x.shape[0]:
+            raise ValueError("UVW x and edge_attr must be matrices with the same rows")
+        from .uvw_conv import lunatp_uvw_conv_func
+
+        graph = self.identity_graph(x.shape[0], x.device)
+        return lunatp_uvw_conv_func(self.rows_op, x, y, weight, graph=graph)
+
+    def __getstate__(self):
+        state = dict(self.__dict__)
+        state["_plan"] = None
+        state["_identity"] = {}
+        return state
 
 
 def _stream(t):

@@ -270,6 +270,9 @@ def lunatp_uvw_conv_func(op, x, edge_attr, weight=None, *, graph: LunaTPGraph, e
     if op.weight_mode == "shared":
         aggregated = op._aggregate(x, edge_attr, env, graph)
         return op._contract(aggregated, weight, N)
+    if graph._tables.get("identity"):
+        # Every edge is its own destination (the row-wise product): no edge graph, no sum.
+        return op._contract(op._aggregate(x, edge_attr, env, graph), weight.contiguous(), E)
     edges = op._edge_graph(graph)
     rows = edges.num_nodes
     xs = x if rows == N else torch.nn.functional.pad(x, (0, 0, 0, rows - N))

@@ -98,6 +98,10 @@ def test_uvw_plan_compiles_without_gpu(tmp_path, monkeypatch):
     assert tp.weight_numel == 45056
     tp.op.plan.precompile()
     assert len(list(tmp_path.glob("uvw_*.co"))) == 3
-    with pytest.raises(NotImplementedError):
-        lunaeq.TensorProduct(ir, sh, ir, uvw_instructions(ir, sh, ir), shared_weights=True,
-                             internal_weights=True, dtype=torch.float64)
+    # fp64 and per-row weights take the row form of the UVW convolution
+    double = lunaeq.TensorProduct(ir, sh, ir, uvw_instructions(ir, sh, ir), shared_weights=True,
+                                  internal_weights=True, dtype=torch.float64)
+    assert double.op.rows_op is not None and double.op.rows_op.agg.spec.startswith("LUNAUVU2 64")
+    per_row = lunaeq.TensorProduct(ir, sh, ir, uvw_instructions(ir, sh, ir), shared_weights=False,
+                                   internal_weights=False)
+    assert per_row.op.rows_op is not None and per_row.op.weight_mode == "external"

@@ -60,3 +60,54 @@ def test_uvw_internal_weights_and_functional_api():
     assert_close(again, ref, torch.float32, "functional")
     out.sum().backward()
     assert tp.weight.grad is not None and tp.weight.grad.shape == (tp.weight_numel,)
+
+
+@pytest.mark.parametrize("dtype,shared", [(torch.float64, True), (torch.float32, False), (torch.float64, False)])
+def test_uvw_rows_fp64_and_per_row_weights(dtype, shared):
+    """fp64 and per-row weights run the row form of the UVW convolution (identity graph)."""
+    from oracle.uvu_conv import conv as oracle_conv
+
+    in1, in2, out, rows = "12x0e+8x1o", "1x0e+2x1o", "8x0e+12x1o+4x2e", 37
+    instructions = uvw_instructions(in1, in2, out)
+    tp = lunaeq.TensorProduct(in1, in2, out, instructions, shared_weights=shared, internal_weights=False,
+                              dtype=dtype)
+    assert tp.op.rows_op is not None
+    gen = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn((tp.weight_numel,) if shared else (rows, tp.weight_numel), generator=gen, dtype=torch.float64)
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ids = torch.arange(rows)
+    ref = oracle_conv(in1, in2, out, instructions, ref_in[0], ref_in[1],
+                      ref_in[2].expand(rows, -1) if shared else ref_in[2], ids, ids, rows)
+    if shared:
+        assert torch.allclose(ref, uvw_tensor_product(in1, in2, out, instructions, x, y, w), atol=1e-12)
+    dev_in = [t.to(DEV, dtype).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in)
+    assert_close(act, ref, dtype, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    ref_first = torch.autograd.grad(ref, ref_in, g, create_graph=True)
+    dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, dtype), create_graph=True)
+    for n, (a, r) in enumerate(zip(dev_first, ref_first)):
+        assert_close(a, r, dtype, f"first-order {n}")
+    dirs = [torch.randn(r.shape, generator=gen, dtype=torch.float64) for r in ref_first]
+    ref_second = torch.autograd.grad(ref_first, ref_in, dirs, allow_unused=True)
+    dev_second = torch.autograd.grad(dev_first, dev_in, [d.to(DEV, dtype) for d in dirs], allow_unused=True)
+    for n, (a, r) in enumerate(zip(dev_second, ref_second)):
+        if r is None:
+            assert a is None or not a.count_nonzero()
+            continue
+        assert_close(torch.zeros_like(r) if a is None else a, r, dtype, f"second-order {n}")
+
+
+def test_uvw_module_dtype_switch():
+    ir, sh = "8x0e+8x1o", "1x0e+1x1o"
+    instructions = uvw_instructions(ir, sh, ir)
+    tp = lunaeq.TensorProduct(ir, sh, ir, instructions, shared_weights=True, internal_weights=True).to(DEV)
+    assert tp.op.rows_op is None
+    tp.double()
+    assert tp.op.compute_dtype == torch.float64 and tp.op.rows_op is not None
+    x = torch.randn(20, tp.irreps_in1.dim, device=DEV, dtype=torch.float64)
+    y = torch.randn(20, tp.irreps_in2.dim, device=DEV, dtype=torch.float64)
+    ref = uvw_tensor_product(ir, sh, ir, instructions, x.cpu(), y.cpu(), tp.weight.detach().cpu())
+    assert_close(tp(x, y), ref, torch.float64, "fp64 after .double()")
