@@ -39,12 +39,16 @@ from .layout import TensorProductPaths
 from .uvu_conv import LunaTPUVUConv, UVUConvForward
 
 
+# Reductions over fewer rows than this stay one library GEMM.
+SPLIT_K_MIN_ROWS = 4096
+
+
 def _split_k_tn(a, b, chunks=16):
     """a^T @ b for tall a [K, M], b [K, N] as `chunks` partial GEMMs and a sum: the
     library GEMM on a long K and a small M x N output leaves most of the chip idle.
     The last K % chunks rows join with one more small GEMM (no padded copies)."""
     K = a.shape[0]
-    if K < 4096:
+    if K < max(SPLIT_K_MIN_ROWS, chunks):
         return a.t() @ b
     step = K // chunks
     main = step * chunks

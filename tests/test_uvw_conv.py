@@ -108,16 +108,19 @@ def test_lowering_and_dispatch():
     assert module.op.compute_dtype == torch.float32
 
 
-def test_split_k_weight_gradient():
+def test_split_k_weight_gradient(monkeypatch):
     """The node-level GEMM's weight gradient is split over K; values and higher
     derivatives equal the plain product's."""
+    from lunaequivariance_amd import uvw_conv
     from lunaequivariance_amd.uvw_conv import _RowsTimesWeight, _split_k_tn
 
     gen = torch.Generator().manual_seed(9)
     a = torch.randn(10001, 30, generator=gen, dtype=torch.float64)
     b = torch.randn(10001, 7, generator=gen, dtype=torch.float64)
     assert torch.allclose(_split_k_tn(a, b), a.t() @ b, atol=1e-11)
-    rows = torch.randn(5000, 3, generator=gen, dtype=torch.float64, requires_grad=True)
+    monkeypatch.setattr(uvw_conv, "SPLIT_K_MIN_ROWS", 16)
+    rows = torch.randn(53, 3, generator=gen, dtype=torch.float64, requires_grad=True)
     weight = torch.randn(3, 2, generator=gen, dtype=torch.float64, requires_grad=True)
+    assert torch.allclose(_split_k_tn(rows, rows[:, :2]), rows.t() @ rows[:, :2], atol=1e-12)
     assert torch.autograd.gradcheck(_RowsTimesWeight.apply, (rows, weight))
     assert torch.autograd.gradgradcheck(_RowsTimesWeight.apply, (rows, weight))
