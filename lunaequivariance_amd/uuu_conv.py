@@ -29,7 +29,7 @@ from . import _native
 from .cg import sparse_terms
 from .graph import LunaTPGraph
 from .layout import TensorProductPaths
-from .uvu_conv import UVUConvForward, _check_device, _stream, l0_feature_layout
+from .uvu_conv import ConvForward, _check_device, _stream, l0_feature_layout
 
 
 def build_uuu_conv_metadata(tp, coefficient_dtype=torch.float32) -> dict:
@@ -319,7 +319,7 @@ def lunatp_uuu_conv_func(op, x, edge_attr, weight=None, *, graph: LunaTPGraph, e
             x, edge_attr, weight, env, ops.graph_tables(graph), graph.num_nodes, bool(return_l0_feat),
             op.torch_config)
         return (out, l0) if return_l0_feat else out
-    return UVUConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
+    return ConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
 
 
 __all__ = ["build_uuu_conv_metadata", "spec_text", "LunaTPUUUConv", "create_uuu_conv_operator",

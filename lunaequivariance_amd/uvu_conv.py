@@ -331,8 +331,9 @@ def _add(a, b):
     return a + b
 
 
-class UVUConvForward(torch.autograd.Function):
-    """Differentiable forward; its backward is ``UVUConvBackward``."""
+class ConvForward(torch.autograd.Function):
+    """Differentiable forward of any convolution operator; its backward is ``ConvBackward``
+    (the reference's ``UVUConvForward``, ``src/lunatp/uvu_conv/interface.py:210-286``)."""
 
     @staticmethod
     def forward(ctx, op, graph, want_l0, x, y, w, env):
@@ -360,10 +361,10 @@ class UVUConvForward(torch.autograd.Function):
 
 def conv_forward(op, graph, want_l0, x, y, w, env):
     """Differentiable forward used by the higher-order rules."""
-    return UVUConvForward.apply(op, graph, want_l0, x, y, w, env)
+    return ConvForward.apply(op, graph, want_l0, x, y, w, env)
 
 
-class UVUConvBackward(torch.autograd.Function):
+class ConvBackward(torch.autograd.Function):
     """Differentiable first-order backward: (x, y, w, env, g, gl0) -> (gx, gy, gw, genv)."""
 
     @staticmethod
@@ -417,7 +418,7 @@ class UVUConvBackward(torch.autograd.Function):
 def conv_backward(op, graph, x, y, w, env, g, gl0, needs=(True, True, True, True)):
     needs = tuple(bool(n) for n in needs)
     if torch.is_grad_enabled():
-        return UVUConvBackward.apply(op, graph, needs, x, y, w, env, g, gl0)
+        return ConvBackward.apply(op, graph, needs, x, y, w, env, g, gl0)
     return op.launch_backward(x, y, w, graph, g, env, gl0, needs)
 
 
@@ -443,9 +444,12 @@ def lunatp_uvu_conv_func(op, x, edge_attr, weight, *, graph: LunaTPGraph, env=No
             x, edge_attr, weight, env, ops.graph_tables(graph), graph.num_nodes, bool(return_l0_feat),
             op.torch_config)
         return (out, l0) if return_l0_feat else out
-    return UVUConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
+    return ConvForward.apply(op, graph, bool(return_l0_feat), x, edge_attr, weight, env)
 
 
-__all__ = ["build_uvu_conv_metadata", "l0_feature_layout", "spec_text", "LunaTPUVUConv",
+# The reference's names for the same autograd nodes.
+UVUConvForward, UVUConvBackward = ConvForward, ConvBackward
+
+__all__ = ["ConvForward", "ConvBackward", "build_uvu_conv_metadata", "l0_feature_layout", "spec_text", "LunaTPUVUConv",
            "create_uvu_conv_operator", "lunatp_uvu_conv_func", "run_forward", "run_backward",
            "NativePlan"]

@@ -36,7 +36,7 @@ import torch
 from .cg import sparse_terms
 from .graph import LunaTPGraph, make_graph
 from .layout import TensorProductPaths
-from .uvu_conv import LunaTPUVUConv, UVUConvForward
+from .uvu_conv import LunaTPUVUConv, ConvForward
 
 
 # Reductions over fewer rows than this stay one library GEMM.
@@ -191,7 +191,7 @@ class LunaTPUVWConv:
             out, _ = torch.ops.lunaeq_amd.uvu_conv_forward(x, y, ones, env, ops.graph_tables(graph),
                                                             graph.num_nodes, False, self.agg.torch_config)
             return out
-        return UVUConvForward.apply(self.agg, graph, False, x, y, ones, env)
+        return ConvForward.apply(self.agg, graph, False, x, y, ones, env)
 
     def _contract(self, values, weight, rows):
         """out[n, o + w*d3 + k] = sum_c W[c, w] A[n, c, k] per output block; weight is the
