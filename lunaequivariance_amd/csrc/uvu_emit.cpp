@@ -855,13 +855,22 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   c.line("  const i64 e0 = (i64)blockIdx.x * 256;");
   c.line("  const int n = E - e0 < 256 ? (int)(E - e0) : 256;");
   for (int col = 0; col < pw; ++col) c.line("  real acc%d = 0;", col);
+  // Consecutive slots with the same column map (the chunks of one group) share
+  // one loop, so the code size does not grow with the channel count.
+  std::vector<std::pair<std::pair<int, int>, const std::vector<std::pair<int, int>>*>> runs;
   for (const auto& kv : by_slot) {
-    c.line("  {");
-    c.line("    const real* src = part + ((i64)%d * E + e0) * PART_W;", kv.first);
+    if (!runs.empty() && runs.back().first.second + 1 == kv.first && *runs.back().second == kv.second)
+      runs.back().first.second = kv.first;
+    else
+      runs.push_back({{kv.first, kv.first}, &kv.second});
+  }
+  for (const auto& run : runs) {
+    c.line("  for (int sl = %d; sl <= %d; ++sl) {", run.first.first, run.first.second);
+    c.line("    const real* src = part + ((i64)sl * E + e0) * PART_W;");
     c.line("    for (int i = t; i < n * (int)PART_W; i += 256) tile[i] = src[i];");
     c.line("    __syncthreads();");
     c.line("    if (t < n) {");
-    for (const auto& pc : kv.second) c.line("      acc%d += tile[t * PART_W + %d];", pc.second, pc.first);
+    for (const auto& pc : *run.second) c.line("      acc%d += tile[t * PART_W + %d];", pc.second, pc.first);
     c.line("    }");
     c.line("    __syncthreads();");
     c.line("  }");

@@ -320,3 +320,61 @@ def test_full_size_sampled_rows(dtype):
                        len(targets))
         (rgx,) = torch.autograd.grad(ref, xs, g64[targets])
         assert_close(gx[node:node + 1], rgx[node:node + 1], dtype, f"gx[{node}]")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_wide_mixed_width_edge_channels(dtype):
+    """Blocks of 65,537 and 65,601 channels, several edge channels, a repeated
+    instruction, env with zeros and scalar features (``tests/lunatp/test_uvu_conv.py:500-575``)."""
+    in1, sh = "65537x0e+65601x1o+1x2e", "2x0e+3x1o+1x2e"
+    out = "65537x0e+65601x0e+65537x1o+65601x1o+1x2e"
+    instructions = [(0, 0, 0, "uvu", True), (0, 0, 0, "uvu", True), (1, 1, 1, "uvu", True),
+                    (0, 1, 2, "uvu", True), (1, 0, 3, "uvu", True)]
+    conv = make_conv(in1, sh, out, instructions, dtype)
+    gen = torch.Generator().manual_seed(92671)
+    src, dst = torch.tensor([1, 0, 1, 0]), torch.tensor([0, 0, 1, 1])
+    x, y, w = inputs(conv, 3, 4, dtype, gen)
+    env = torch.tensor([0.0, 0.5, -1.0, 0.0], dtype=torch.float64)
+    check_orders(conv, in1, sh, out, instructions, x, y, w, src, dst, 3, dtype, gen, env=env, l0=True, orders=2)
+
+
+def test_graph_capture_replays():
+    """Forward and first-order backward captured in a HIP graph and replayed with new
+    inputs each time, every replay against eager (``tests/lunatp/test_uvu_conv.py:933-995``)."""
+    dtype = torch.float32
+    in1, sh, out, instructions = mace_irreps(16, 2)
+    conv = make_conv(in1, sh, out, instructions, dtype)
+    gen = torch.Generator().manual_seed(12)
+    src, dst = random_graph(40, 300, gen)
+    graph = conv.create_graph(src.to(DEV), dst.to(DEV), 40)
+    x, y, w = (t.to(DEV, dtype) for t in inputs(conv, 40, 300, dtype, gen))
+    g = torch.randn(40, conv.irreps_out.dim, generator=gen).to(DEV)
+    sx, sy, sw, sg = (t.clone().requires_grad_(t is not g) if t is not g else t.clone() for t in (x, y, w, g))
+
+    def step():
+        o = conv(sx, sy, sw, graph=graph)
+        return (o, *torch.autograd.grad(o, (sx, sy, sw), sg))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    captured = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(captured):
+        static = step()
+    for replay in range(3):
+        nx, ny, nw, ng = (torch.randn(t.shape, generator=gen).to(DEV) for t in (x, y, w, g))
+        with torch.no_grad():
+            sx.copy_(nx)
+            sy.copy_(ny)
+            sw.copy_(nw)
+            sg.copy_(ng)
+        captured.replay()
+        torch.cuda.synchronize()
+        ex, ey, ew = (t.clone().requires_grad_() for t in (nx, ny, nw))
+        eo = conv(ex, ey, ew, graph=graph)
+        expected = (eo, *torch.autograd.grad(eo, (ex, ey, ew), ng))
+        for n, (a, b) in enumerate(zip(static, expected)):
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-6), f"replay {replay}, output {n}"
