@@ -2,9 +2,7 @@
 
 Mirrors ``prepare_tensor_product`` / ``tensor_product_conv``
 (``src/lunatp/interface.py:147-262``) for the UVU, UUU and UVW convolutions
-and the shared-weight UVW product.  The non-convolution uuu/uvu products of
-the reference are outside this library's scope and raise
-``NotImplementedError``.
+and the row-wise products of all three modes.
 """
 
 from __future__ import annotations
@@ -58,7 +56,9 @@ def prepare_tensor_product(irreps_in1, irreps_in2=None, irreps_out=None, instruc
         if inferred == "uvw":
             from .uvw import LunaTPUVW
             return LunaTPUVW(paths, dtype=dtype)
-        _unsupported(inferred, False)
+        from .rowwise import LunaTPRows
+
+        return LunaTPRows(paths, dtype=dtype)
     if inferred == "uuu":
         return create_uuu_conv_operator(paths, dtype=dtype)
     if inferred == "uvw":
@@ -100,7 +100,7 @@ def tensor_product(x, y, weight=None, *, irreps_in1=None, irreps_in2=None, irrep
                    instructions=None, in1_var=None, in2_var=None, out_var=None,
                    irrep_normalization=None, path_normalization=None, shared_weights=False,
                    config=None):
-    """Independent per-row tensor products (``lunatp/interface.py:210-235``); UVW only here."""
+    """Independent per-row tensor products (``lunatp/interface.py:210-235``)."""
     if config is None:
         config = _config_from_arguments(x, irreps_in1, irreps_in2, irreps_out, instructions,
                                         in1_var, in2_var, out_var, irrep_normalization,

@@ -16,10 +16,10 @@ from .uvu_conv import create_uvu_conv_operator
 class TensorProduct(torch.nn.Module):
     """Row-wise tensor product (``src/modules/tensorproduct.py:19-116``).
 
-    This build provides the ``uvw`` connection: shared weights in fp32 on
-    matrix-core kernels, fp64 and per-row weights through the row form of the
-    UVW convolution.  Weights are the configuration's registered parameter
-    unless given.
+    ``uvw``: shared weights in fp32 on matrix-core kernels, fp64 and per-row
+    weights through the row form of the UVW convolution.  ``uvu`` and ``uuu``:
+    the convolution kernels over the identity graph (matrices only).  Weights
+    are the configuration's registered parameter unless given.
     """
 
     def __init__(self, irreps_in1, irreps_in2=None, irreps_out=None, instructions=None,
@@ -47,14 +47,10 @@ class TensorProduct(torch.nn.Module):
         if len(modes) != 1 or not modes <= {"uuu", "uvu", "uvw"}:
             raise ValueError("TensorProduct requires one connection mode: uuu, uvu or uvw")
         self.mode = modes.pop()
-        if self.mode != "uvw":
-            raise NotImplementedError(f"{self.mode} tensor products are not part of this MI355X build")
-        from .uvw import LunaTPUVW
-
         weight = getattr(tp, "weight", None)
         if dtype is None:
-            dtype = weight.dtype if isinstance(weight, torch.Tensor) and weight.numel() else torch.float32
-        self.op = LunaTPUVW(tp, dtype=dtype)
+            dtype = weight.dtype if isinstance(weight, torch.Tensor) else torch.float32
+        self.op = self._make_op(tp, dtype)
         self.tp = tp
         self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
         self.instructions = tp.instructions
@@ -65,13 +61,20 @@ class TensorProduct(torch.nn.Module):
     def weight(self):
         return self.tp.weight
 
-    def _apply(self, fn, recurse=True):
-        from .uvw import LunaTPUVW
+    def _make_op(self, tp, dtype):
+        if self.mode == "uvw":
+            from .uvw import LunaTPUVW
 
+            return LunaTPUVW(tp, dtype=dtype)
+        from .rowwise import LunaTPRows
+
+        return LunaTPRows(tp, dtype=dtype)
+
+    def _apply(self, fn, recurse=True):
         dtype = fn(torch.empty(0, dtype=self.op.compute_dtype)).dtype
         result = super()._apply(fn, recurse=recurse)
         if dtype in (torch.float32, torch.float64) and dtype != self.op.compute_dtype:
-            self.op = LunaTPUVW(self.tp, dtype=dtype)
+            self.op = self._make_op(self.tp, dtype)
         return result
 
     def forward(self, x, y, weight=None):

@@ -1,0 +1,73 @@
+"""Row-wise UVU and UUU tensor products on the convolution kernels.
+
+A row-wise product (``TensorProduct``, ``src/modules/tensorproduct.py:19-116``;
+the reference's ``LunaTPUVU`` / ``LunaTPUUU``, ``src/lunatp/interface.py:265-307``)
+is the convolution over the identity graph: row b is node b, edge b and the
+destination of edge b, so the HIP convolution kernels compute it with every
+segment holding one edge.  Shared weights ``[weight_numel]`` are broadcast to
+every row.  Inputs are matrices ``[B, dim]`` (the reference's UUU also
+broadcasts leading batch dimensions; that is not provided here).
+"""
+
+from __future__ import annotations
+
+from copy import copy
+
+import torch
+
+from .graph import make_graph
+from .layout import TensorProductPaths
+
+
+class LunaTPRows:
+    """Prepared row-wise uvu or uuu product."""
+
+    def __init__(self, tp, *, dtype=torch.float32):
+        paths = TensorProductPaths.from_tensor_product(tp)
+        modes = {ins.connection_mode for ins in paths.instructions}
+        if len(modes) != 1 or not modes <= {"uvu", "uuu"}:
+            raise ValueError("row-wise products here take one connection mode: uvu or uuu")
+        self.mode = modes.pop()
+        if dtype not in (torch.float32, torch.float64):
+            raise ValueError(f"{self.mode} requires float32 or float64, got {dtype}")
+        self.compute_dtype = dtype
+        self.shared_weights = bool(paths.shared_weights)
+        # The convolution lowering takes per-edge weights; shared rows are broadcast at run time.
+        flat = copy(paths)
+        flat.shared_weights = False
+        flat.internal_weights = False
+        if self.mode == "uvu":
+            from .uvu_conv import create_uvu_conv_operator
+
+            self.conv = create_uvu_conv_operator(flat, dtype=dtype)
+        else:
+            from .uuu_conv import create_uuu_conv_operator
+
+            self.conv = create_uuu_conv_operator(flat, dtype=dtype)
+        self.weight_numel = self.conv.weight_numel
+        self.out_dim = self.conv.out_dim
+        self._identity = {}
+
+    def identity_graph(self, rows, device):
+        key = (rows, str(device))
+        if key not in self._identity:
+            ids = torch.arange(rows, device=device)
+            self._identity = {key: make_graph(ids, ids, rows)}
+        return self._identity[key]
+
+    def run(self, x, y, weight=None):
+        if x.ndim != 2 or y.ndim != 2 or x.shape[0] != y.shape[0]:
+            raise ValueError(f"{self.mode} row-wise inputs must be matrices with the same rows")
+        rows = x.shape[0]
+        if weight is not None and weight.shape in ((self.weight_numel,), (1, self.weight_numel)):
+            weight = weight.reshape(1, -1).expand(rows, -1)
+        graph = self.identity_graph(rows, x.device)
+        return self.conv.run(x, y, weight, graph=graph)
+
+    def __getstate__(self):
+        state = dict(self.__dict__)
+        state["_identity"] = {}
+        return state
+
+
+__all__ = ["LunaTPRows"]

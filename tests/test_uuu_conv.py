@@ -255,3 +255,20 @@ def test_weight_linear_part():
     assert int(lin.spec.split()[6]) == len(mixed) - 2
     assert not lin.l0_complete and op.l0_complete
     assert restore_operator(lin.torch_config).active_specs == lin.active_specs
+
+
+def test_rowwise_products_dispatch():
+    """Row-wise uvu / uuu products are prepared on the convolution operators."""
+    import lunaequivariance_amd as lunaeq
+    from lunaequivariance_amd.rowwise import LunaTPRows
+
+    ir = "4x0e+4x1o"
+    uuu = uuu_paths(ir, ir, ir)
+    op = lunaeq.prepare_tensor_product(ir, ir, ir, uuu, shared_weights=True)
+    assert isinstance(op, LunaTPRows) and op.mode == "uuu" and op.shared_weights
+    a, b = lunaeq.Irreps(ir), lunaeq.Irreps("1x0e+1x1o")
+    uvu = [(i, j, k, "uvu", True) for i, (_, p) in enumerate(a) for j, (_, q) in enumerate(b)
+           for k, (_, r) in enumerate(a) if r in p * q]
+    module = lunaeq.TensorProduct(ir, "1x0e+1x1o", ir, uvu, shared_weights=False, internal_weights=False,
+                                  dtype=torch.float64)
+    assert module.mode == "uvu" and module.op.conv.compute_dtype == torch.float64
