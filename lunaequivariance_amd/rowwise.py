@@ -5,8 +5,8 @@ the reference's ``LunaTPUVU`` / ``LunaTPUUU``, ``src/lunatp/interface.py:265-307
 is the convolution over the identity graph: row b is node b, edge b and the
 destination of edge b, so the HIP convolution kernels compute it with every
 segment holding one edge.  Shared weights ``[weight_numel]`` are broadcast to
-every row.  Inputs are matrices ``[B, dim]`` (the reference's UUU also
-broadcasts leading batch dimensions; that is not provided here).
+every row.  UVU takes matrices ``[B, dim]``; UUU also broadcasts leading batch
+dimensions of x, y and per-row weights, as the reference does.
 """
 
 from __future__ import annotations
@@ -56,6 +56,10 @@ class LunaTPRows:
         return self._identity[key]
 
     def run(self, x, y, weight=None):
+        if self.mode == "uuu" and (x.ndim != 2 or y.ndim != 2 or x.shape[0] != y.shape[0]
+                                   or (weight is not None and weight.ndim > 1
+                                       and weight.shape[:-1] != x.shape[:-1])):
+            return self._run_broadcast(x, y, weight)
         if x.ndim != 2 or y.ndim != 2 or x.shape[0] != y.shape[0]:
             raise ValueError(f"{self.mode} row-wise inputs must be matrices with the same rows")
         rows = x.shape[0]
@@ -63,6 +67,16 @@ class LunaTPRows:
             weight = weight.reshape(1, -1).expand(rows, -1)
         graph = self.identity_graph(rows, x.device)
         return self.conv.run(x, y, weight, graph=graph)
+
+    def _run_broadcast(self, x, y, weight):
+        """UUU with leading batch dimensions broadcast as in PyTorch
+        (``docs/operators/tensor_product.md:48-54``): flatten, run, reshape."""
+        shared = weight is None or weight.ndim == 1
+        shapes = [x.shape[:-1], y.shape[:-1]] + ([] if shared else [weight.shape[:-1]])
+        lead = torch.broadcast_shapes(*shapes)
+        flat = lambda t: t.expand(*lead, t.shape[-1]).reshape(-1, t.shape[-1])  # noqa: E731
+        out = self.run(flat(x), flat(y), weight if shared else flat(weight))
+        return out.reshape(*lead, out.shape[-1])
 
     def __getstate__(self):
         state = dict(self.__dict__)

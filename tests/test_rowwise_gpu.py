@@ -80,3 +80,17 @@ def test_rowwise_internal_weights_and_functional():
     op = lunaeq.prepare_tensor_product(in1, in2, out, ins, shared_weights=True)
     again = lunaeq.tensor_product(x, y, tp.weight.detach(), config=op)
     assert_close(again, ref, torch.float32, "functional")
+
+
+def test_uuu_batch_broadcasting():
+    """UUU broadcasts leading dimensions (docs/operators/tensor_product.md:108-130 example shapes)."""
+    ins = [(0, 0, 0, "uuu", True)]
+    tp = lunaeq.TensorProduct("8x1o", "8x1o", "8x0e", ins, shared_weights=False, internal_weights=False)
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(4, 1, 24, generator=gen)
+    y = torch.randn(1, 3, 24, generator=gen)
+    w = torch.randn(4, 3, 8, generator=gen)
+    out = tp(x.to(DEV), y.to(DEV), w.to(DEV))
+    assert out.shape == (4, 3, 8)
+    expected = (x.reshape(4, 1, 8, 3) * y.reshape(1, 3, 8, 3)).sum(-1) * w / 3 ** 0.5
+    assert_close(out, expected.double(), torch.float32, "broadcast")
