@@ -1,6 +1,7 @@
-"""Writes the golden fixtures of the UVU convolution from the CPU oracle.
+"""Writes the golden fixtures of the UVU, UUU and UVW convolutions from the CPU oracle.
 
-Run from the repository root: ``python tests/golden/make_golden.py``.
+Run from the repository root: ``python tests/golden/make_golden.py [names...]``
+(all fixtures, or only the named uuu/uvw ones).
 Each ``.npz`` holds the problem (irreps, instructions, graph, inputs) and
 fp64 outputs: the forward, first-order gradients for a seed ``g`` and
 second-order derivatives of ``<gx,rx> + <gy,ry> + <gw,rw>`` for directions
@@ -33,9 +34,19 @@ def all_paths(in1, in2, out):
     return result
 
 
-def weight_numel(in1, in2, instructions):
+def weight_numel(in1, in2, instructions, out=None):
+    """Weights per edge: mul1*mul2 per uvu path, mul1 per weighted uuu path, mul1*mul2*mul3 per uvw path."""
     a, b = parse_irreps(in1), parse_irreps(in2)
-    return sum(a[i][0] * b[j][0] for i, j, *_ in instructions)
+    c = parse_irreps(out) if out is not None else None
+    total = 0
+    for i, j, k, mode, has_w, *_ in instructions:
+        if mode == "uvu":
+            total += a[i][0] * b[j][0]
+        elif mode == "uuu":
+            total += a[i][0] if has_w else 0
+        else:
+            total += a[i][0] * b[j][0] * c[k][0]
+    return total
 
 
 def make_case(name, in1, in2, out, instructions, nodes, src, dst, seed, env=False):
@@ -44,7 +55,7 @@ def make_case(name, in1, in2, out, instructions, nodes, src, dst, seed, env=Fals
     E = len(src)
     x = torch.randn(nodes, dims[0], generator=gen, dtype=torch.float64)
     y = torch.randn(E, dims[1], generator=gen, dtype=torch.float64)
-    w = torch.randn(E, weight_numel(in1, in2, instructions), generator=gen, dtype=torch.float64)
+    w = torch.randn(E, weight_numel(in1, in2, instructions, out), generator=gen, dtype=torch.float64)
     e = torch.rand(E, generator=gen, dtype=torch.float64) if env else None
     g = torch.randn(nodes, dims[2], generator=gen, dtype=torch.float64)
     rx, ry, rw = (torch.randn(t.shape, generator=gen, dtype=torch.float64) for t in (x, y, w))
@@ -65,7 +76,9 @@ def make_case(name, in1, in2, out, instructions, nodes, src, dst, seed, env=Fals
     )
 
 
-def main():
+def main(only=None):
+    if only:
+        return extra_cases(only)
     # The reference's standard problem shape (tests/conftest.py:8-70): 7 nodes, 19 edges.
     gen = torch.Generator().manual_seed(731)
     src = torch.randint(7, (19,), generator=gen)
@@ -100,7 +113,26 @@ def main():
     src = torch.randint(12, (60,), generator=gen)
     dst = torch.sort(torch.randint(12, (60,), generator=gen))[0]
     make_case("lmax3_paths", in1, sh, "+".join(outs), instructions, 12, src, dst, 3)
+    extra_cases(None)
+
+
+def extra_cases(only):
+    """The uuu and uvw convolutions on the reference's standard problem shape."""
+    gen = torch.Generator().manual_seed(731)
+    src = torch.randint(7, (19,), generator=gen)
+    dst = torch.sort(torch.randint(7, (19,), generator=gen))[0]
+    ir = "32x0e+32x1o"
+    if not only or "uuu_reference" in only:
+        a = parse_irreps(ir)
+        uuu = [(i, j, k, "uuu", n != 1) for n, (i, j, k) in enumerate(
+            (i, j, k) for i, (_, l1, p1) in enumerate(a) for j, (_, l2, p2) in enumerate(a)
+            for k, (_, l3, p3) in enumerate(a) if abs(l1 - l2) <= l3 <= l1 + l2 and p1 * p2 == p3)]
+        make_case("uuu_reference", ir, ir, ir, uuu, 7, src, dst, 733, env=True)
+    if not only or "uvw_reference" in only:
+        sh, narrow = "1x0e+1x1o", "16x0e+16x1o"  # 16 channels keep the per-edge uvw weights small
+        uvw = [(i, j, k, "uvw", True) for i, j, k, *_ in all_paths(narrow, sh, narrow)]
+        make_case("uvw_reference", narrow, sh, narrow, uvw, 7, src, dst, 734, env=True)
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:] or None)

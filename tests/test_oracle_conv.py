@@ -135,7 +135,8 @@ def load_golden(name):
     return meta, {k: torch.tensor(data[k]) for k in data.files if k != "meta"}
 
 
-@pytest.mark.parametrize("name", ["reference_problem", "config1_small", "multi_edge_env", "lmax3_paths"])
+@pytest.mark.parametrize("name", ["reference_problem", "config1_small", "multi_edge_env", "lmax3_paths",
+                                  "uuu_reference", "uvw_reference"])
 def test_golden_fixtures(name):
     """The oracle still reproduces its committed fixtures (forward, first and second order)."""
     meta, t = load_golden(name)

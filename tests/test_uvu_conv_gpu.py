@@ -255,7 +255,8 @@ def load_golden(name):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-@pytest.mark.parametrize("name", ["reference_problem", "config1_small", "multi_edge_env", "lmax3_paths"])
+@pytest.mark.parametrize("name", ["reference_problem", "config1_small", "multi_edge_env", "lmax3_paths",
+                                  "uuu_reference", "uvw_reference"])
 def test_golden_fixtures(name, dtype):
     """HIP forward, first and second order against the committed oracle fixtures."""
     meta, t = load_golden(name)
