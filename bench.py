@@ -40,6 +40,8 @@ CONFIGS = {
     "uuu_l2": dict(channels=64, atoms=2083, lmax=2, dtype="float32"),
     "uuu_l3": dict(channels=64, atoms=2083, lmax=3, dtype="float32"),
     "uuu_l4": dict(channels=64, atoms=2083, lmax=4, dtype="float32"),
+    "uuu_l5": dict(channels=64, atoms=2083, lmax=5, dtype="float32"),
+    "uuu_l6": dict(channels=64, atoms=2083, lmax=6, dtype="float32"),
     # UVW conv (docs/operators/tensor_product_conv.md:266-292): the same graph, 64 channels
     # per degree, edge features = one spherical-harmonic channel per degree, shared weights.
     "uvw_l2": dict(channels=64, atoms=2083, lmax=2, dtype="float32", mode="uvw"),

@@ -67,7 +67,8 @@ struct UGroup {
   int phase = 0;                 // backward: launch order among groups sharing edge blocks
   int genv_slot = 0;             // backward: first partial slot of env's gradient
   std::set<int> xbs, ybs, obs;
-  std::set<int> gy_accumulate;   // backward: y blocks already written by an earlier phase
+  std::set<int> gx_accumulate;   // backward: x blocks already written by an earlier phase
+  std::set<int> out_accumulate;  // forward: output blocks already written by an earlier launch
 };
 
 struct UuuPlan {
@@ -201,12 +202,26 @@ int cost(const USpec& s, const std::vector<int>& paths, bool backward) {
   return regs * (s.bits / 32);
 }
 
-// Forward: paths writing one output block stay together (plain stores, no
-// collisions); output blocks of one channel count are packed into a group
-// while its register estimate fits.
+// Forward: the unit is an edge block (every path reading it), so each
+// per-edge row of y and w is read by one group only; a unit over the register
+// estimate is cut by output block.  Units of one channel count are packed into
+// a group while its estimate fits.  The output rows are per node: a group whose
+// output block an earlier group (launch) already wrote adds to it.
 std::vector<UGroup> forward_groups(const USpec& s) {
-  std::vector<std::vector<int>> units(s.oblocks.size());
-  for (int p = 0; p < (int)s.paths.size(); ++p) units[s.paths[p].ob].push_back(p);
+  std::vector<std::vector<int>> units;
+  for (int b = 0; b < (int)s.yblocks.size(); ++b) {
+    std::vector<int> unit;
+    for (int p = 0; p < (int)s.paths.size(); ++p)
+      if (s.paths[p].yb == b) unit.push_back(p);
+    if (unit.empty()) continue;
+    if (cost(s, unit, false) <= kForwardBudget) {
+      units.push_back(unit);
+      continue;
+    }
+    std::map<int, std::vector<int>> by_out;
+    for (int p : unit) by_out[s.paths[p].ob].push_back(p);
+    for (const auto& kv : by_out) units.push_back(kv.second);
+  }
   std::vector<UGroup> groups;
   std::map<int, int> open;  // channels -> index of the group being filled
   for (const auto& unit : units) {
@@ -225,27 +240,37 @@ std::vector<UGroup> forward_groups(const USpec& s) {
     groups.push_back(g);
     open[ch] = (int)groups.size() - 1;
   }
-  for (UGroup& g : groups) finish_group(g, s);
+  std::set<int> written;
+  for (UGroup& g : groups) {
+    std::sort(g.paths.begin(), g.paths.end());
+    finish_group(g, s);
+    for (int b : g.obs)
+      if (written.count(b)) g.out_accumulate.insert(b);
+    written.insert(g.obs.begin(), g.obs.end());
+  }
   return groups;
 }
 
-// Backward: a group owns whole input blocks (gx stays in registers) and, when
-// it fits, whole connected sets of input and edge blocks (gy in registers).
-// A connected set over budget is cut by input block into groups of distinct
-// phases; a later phase adds its share of gy to what the earlier one wrote.
+// Backward: a group owns whole edge blocks (gy of an edge is complete in
+// registers and written once) and, when it fits, whole connected sets of input
+// and edge blocks (gx complete too).  A connected set over budget is cut by
+// edge block into groups of distinct phases; a later phase adds its share of
+// gx to what an earlier one wrote.  Cutting by edge block keeps every
+// per-edge row (y, w, gy, gw) read or written once; only the per-node rows
+// (x, the g[dst] gather, gx) are touched by several phases.
 std::vector<UGroup> backward_groups(const USpec& s, int* phases) {
   const int nx = (int)s.xblocks.size();
   std::vector<int> root(nx + s.yblocks.size());
   for (size_t n = 0; n < root.size(); ++n) root[n] = (int)n;
   std::function<int(int)> find = [&](int a) { return root[a] == a ? a : root[a] = find(root[a]); };
   for (const UPath& p : s.paths) root[find(p.xb)] = find(nx + p.yb);
-  std::map<int, std::vector<int>> components;  // root -> input blocks, in order
+  std::map<int, std::vector<int>> components;  // root -> edge blocks, in order
   std::vector<int> component_order;
-  for (int b = 0; b < nx; ++b) {
+  for (int b = 0; b < (int)s.yblocks.size(); ++b) {
     bool used = false;
-    for (const UPath& p : s.paths) used |= p.xb == b;
+    for (const UPath& p : s.paths) used |= p.yb == b;
     if (!used) continue;
-    const int r = find(b);
+    const int r = find(nx + b);
     if (!components.count(r)) component_order.push_back(r);
     components[r].push_back(b);
   }
@@ -257,7 +282,7 @@ std::vector<UGroup> backward_groups(const USpec& s, int* phases) {
     for (int b : components[r]) {
       std::vector<int> block;
       for (int p = 0; p < (int)s.paths.size(); ++p)
-        if (s.paths[p].xb == b) block.push_back(p);
+        if (s.paths[p].yb == b) block.push_back(p);
       std::vector<int> merged = current;
       merged.insert(merged.end(), block.begin(), block.end());
       if (!current.empty() && cost(s, merged, true) > kBackwardBudget) {
@@ -275,9 +300,9 @@ std::vector<UGroup> backward_groups(const USpec& s, int* phases) {
       std::sort(g.paths.begin(), g.paths.end());
       g.phase = (int)n;
       finish_group(g, s);
-      for (int b : g.ybs)
-        if (written.count(b)) g.gy_accumulate.insert(b);
-      written.insert(g.ybs.begin(), g.ybs.end());
+      for (int b : g.xbs)
+        if (written.count(b)) g.gx_accumulate.insert(b);
+      written.insert(g.xbs.begin(), g.xbs.end());
       groups.push_back(g);
     }
     *phases = std::max(*phases, (int)parts.size());
@@ -547,7 +572,8 @@ std::string emit_forward(const UuuPlan& plan, bool env, bool l0) {
     c.line("      real* orow = out + (i64)node * OUTD;");
     for (int b : g.obs)
       for (int k = 0; k < s.oblocks[b].d; ++k)
-        c.line("      orow[%d + u * %d] = o%d_%d;", s.oblocks[b].off + k, s.oblocks[b].d, b, k);
+        c.line("      orow[%d + u * %d] %s o%d_%d;", s.oblocks[b].off + k, s.oblocks[b].d,
+               g.out_accumulate.count(b) ? "+=" : "=", b, k);
     c.line("    }");
     c.line("  }");
     c.line("}");
@@ -672,10 +698,7 @@ std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx,
       for (int b : g.ybs)
         for (int j = 0; j < s.yblocks[b].d; ++j) {
           const long off = s.yblocks[b].off + j;
-          if (g.gy_accumulate.count(b))
-            c.line("        gy[(i64)e * IN2 + %ld + (i64)u * %d] += gy%d_%d;", off, s.yblocks[b].d, b, j);
-          else
-            c.line("        gy[(i64)e * IN2 + %ld + (i64)u * %d] = gy%d_%d;", off, s.yblocks[b].d, b, j);
+          c.line("        gy[(i64)e * IN2 + %ld + (i64)u * %d] = gy%d_%d;", off, s.yblocks[b].d, b, j);
         }
     c.line("      }");
     if (want_genv) {
@@ -692,7 +715,8 @@ std::string emit_backward(const UuuPlan& plan, bool env, bool gl0, bool want_gx,
       c.line("      real* xrow = gx + (i64)node * IN1;");
       for (int b : g.xbs)
         for (int i = 0; i < s.xblocks[b].d; ++i)
-          c.line("      xrow[%d + u * %d] = gx%d_%d;", s.xblocks[b].off + i, s.xblocks[b].d, b, i);
+          c.line("      xrow[%d + u * %d] %s gx%d_%d;", s.xblocks[b].off + i, s.xblocks[b].d,
+                 g.gx_accumulate.count(b) ? "+=" : "=", b, i);
       c.line("    }");
     }
     c.line("  }");
