@@ -79,7 +79,7 @@ def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the operator shards by destination-node ranges; see DESIGN.md)", file=sys.stderr)
+              "(the operator would shard by destination-node ranges)", file=sys.stderr)
         sys.exit(2)
     import torch
 
