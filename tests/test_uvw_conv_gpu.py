@@ -135,3 +135,24 @@ def test_internal_weights_train():
     out.sum().backward()
     (gw,) = torch.autograd.grad(ref.sum(), weight)
     assert_close(module.weight.grad, gw, torch.float64, "internal weight gradient")
+
+
+@pytest.mark.parametrize("mode", ["uvu", "uuu", "uvw"])
+def test_zero_nodes(mode):
+    """A graph with no nodes and no edges gives empty outputs and gradients in every mode."""
+    ir = "4x0e+4x1o"
+    edge = ir if mode == "uuu" else "1x0e+1x1o"
+    a, b = lunaeq.Irreps(ir), lunaeq.Irreps(edge)
+    ins = [(i, j, k, mode, True) for i, (m, p) in enumerate(a) for j, (n, q) in enumerate(b)
+           for k, (o, r) in enumerate(a) if r in p * q and (mode != "uuu" or m == n == o)]
+    module = lunaeq.TensorProductConv(ir, edge, ir, ins, internal_weights=False, shared_weights=False)
+    empty = torch.zeros(0, dtype=torch.int64, device=DEV)
+    graph = module.create_graph(empty, empty, 0)
+    x = torch.randn(0, a.dim, device=DEV, requires_grad=True)
+    y = torch.randn(0, b.dim, device=DEV, requires_grad=True)
+    w = torch.randn(0, module.weight_numel, device=DEV, requires_grad=True)
+    out = module(x, y, w, graph=graph)
+    assert out.shape == (0, a.dim)
+    grads = torch.autograd.grad(out.sum(), (x, y, w), allow_unused=True)
+    for value, grad in zip((x, y, w), grads):
+        assert grad is None or grad.shape == value.shape
