@@ -5,9 +5,10 @@
 //   Z_p[b, k, K=(u,v)] = sum_{(i,j)} c_ijk x[b, xo + u*d1 + i] y[b, yo + v*d2 + j]
 //   out[b, oo + w*d3 + k] += sum_K Z_p[b, k, K] W_p[K, w]        (W_p = w[wo + K*mul3 + w])
 // (e3nn's uvw connection, src/lunatp/uvw/kernels/forward.py:1082-1465).  The
-// sparse CG producer is VALU work staged into LDS; the contraction over K is
-// v_mfma_f32_32x32x2f32 with a 32-row tile of b as M and 32 output channels
-// as N.  The backward is two more matrix-core passes:
+// sparse CG producer is VALU work on rows staged through LDS; the contraction
+// over K is v_mfma_f32_32x32x2f32 with 32 output channels (one tile) or 64
+// (two tiles fed by one Z operand) as M and a 32-row tile of b as N.  The
+// backward is two more matrix-core passes:
 //   dZ_p[b, k, K] = sum_w g[b, oo + w*d3 + k] W_p[K, w]  ->  gx, gy through the CG terms
 //   dW_p[K, w]    = sum_{b,k} Z_p[b, k, K] g[b, oo + w*d3 + k]   (per row chunk, then reduced)
 #include <algorithm>
@@ -40,7 +41,7 @@ struct UvwSpec {
   std::vector<UvwPath> paths;
 };
 
-constexpr int kChunkRows = 256;  // batch rows per wave (and per partial) of the weight gradient
+constexpr int kChunkRows = 256;  // default batch rows per wave (and per partial) of the weight gradient
 constexpr int kReduceGroups = 16;  // parallel groups of partials in the weight-gradient reduction
 
 int read_int(std::istringstream& in, const char* what) {
@@ -214,6 +215,40 @@ bool staged_path(const UvwSpec& s, const UvwPath& q) {
 }
 
 
+// Forward units computed 64 output channels per wave (two 32-wide matrix
+// tiles fed by one Z operand, so the sparse CG work and the x staging are
+// shared by twice the matrix work; weights staged per chunk through LDS).
+// Needs every path staged and at most 5 output components (160 accumulators).
+bool wide_unit(const UvwSpec& s, const Unit& u) {
+  const char* e = std::getenv("LUNAEQ_AMD_UVW_WIDE");
+  if (e && std::atoi(e) == 0) return false;
+  const UvwPath& head = s.paths[u.paths[0]];
+  if (head.d3 > 5 || head.mul3 <= 32) return false;
+  for (int p : u.paths)
+    if (!staged_path(s, s.paths[p])) return false;
+  return true;
+}
+
+// Wide units whose chunks go straight from HBM into LDS (global_load_lds,
+// double-buffered: the next chunk streams in while the current one is used):
+// weights need 16-byte aligned rows, and mul1 whole chunks of kDmaU channels.
+constexpr int kDmaU = 8;
+bool dma_unit(const UvwSpec& s, const Unit& u) {
+  const char* e = std::getenv("LUNAEQ_AMD_UVW_WIDE");
+  if (e && std::atoi(e) != 2) return false;
+  if (!wide_unit(s, u)) return false;
+  for (int p : u.paths) {
+    const UvwPath& q = s.paths[p];
+    if (q.mul3 % 4 || q.w_off % 4 || q.mul1 % kDmaU || q.d1 > 7) return false;
+  }
+  return true;
+}
+
+int fwd_tiles(const UvwSpec& s, const Unit& u) {
+  const int mul3 = s.paths[u.paths[0]].mul3;
+  return wide_unit(s, u) ? (mul3 + 63) / 64 : (mul3 + 31) / 32;
+}
+
 // Backward paths whose seed rows and weights are staged through LDS in
 // chunks of 16 output channels.
 bool staged_seeds(const UvwSpec& s, const UvwPath& q) {
@@ -236,6 +271,9 @@ const char* kPrelude = R"(
 typedef float real;
 typedef long long i64;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) float lreal;
+typedef __attribute__((address_space(3))) float4 lfloat4;
+typedef __attribute__((address_space(3))) void lvoid;
 #define FMA(a, b, c) __builtin_fmaf((a), (b), (c))
 // D[i][j] += sum_{k<2} A[i][k] B[k][j]; lane l supplies A[l%32][l/32] and
 // B[l/32][l%32]; register r of lane l holds D[8(r/4) + 4(l/32) + r%4][l%32].
@@ -252,15 +290,248 @@ void emit_head(Code& c) {
 
 // ---------------------------------------------------------------- forward
 // out^T[w, b] = sum_p sum_K W_p[K, w] Z_p[b, K] per output component k, on
-// the matrix cores with A = W_p^T (rows w, 32 output channels per wave), B =
+// the matrix cores with A = W_p^T (rows w, 32 or 64 output channels per wave), B =
 // Z_p (32 batch rows per wave), K = (u, v) two per instruction.  Each lane
 // produces its own B operand, Z_p[b0 + col, K = 2s + hk, k] for every k, from
 // the x and y rows of its batch row (the sparse CG terms as VALU work).
+// One wide unit (see wide_unit): a wave owns 32 batch rows and output channels
+// w0 .. w0+63; register r of tile t holds channel w0 + 32t + 8(r/4) + 4hk + r%4
+// of batch row b0 + col.
+void emit_forward_wide(Code& c, const UvwSpec& s, const Unit& u, int nt) {
+  const UvwPath& head = s.paths[u.paths[0]];
+  const int d3 = head.d3, mul3 = head.mul3;
+  c.line("  if (unit < %d) {", nt);
+  c.line("    const int w0 = unit * 64;");
+  for (int t = 0; t < 2; ++t)
+    for (int k = 0; k < d3; ++k) c.line("    floatx16 acc%d_%d = (floatx16)(0.0f);", t, k);
+  for (int p : u.paths) {
+    const UvwPath& q = s.paths[p];
+    const std::set<int> is = term_is(q), js = term_js(q);
+    const int chd = kStageU * q.d1;
+    const bool wvec = mul3 % 4 == 0 && q.w_off % 4 == 0;
+    c.line("    {");
+    c.line("      const real* yr = y + (i64)brow * %d + %d;", s.in2, q.y_off);
+    for (int j : js) c.line("      const real y%d = yr[%d];", j, j);
+    c.line("      for (int c0 = 0; c0 < %d; c0 += %d) {", q.mul1, kStageU);
+    c.line("        {");
+    // x rows of the chunk: consecutive lanes on consecutive 16-byte pieces.
+    c.line("        const float4* xg = (const float4*)(x + %d + c0 * %d);", q.x_off, q.d1);
+    c.line("        #pragma unroll 2");
+    c.line("        for (int it = 0; it < %d; ++it) {", (32 * chd / 4 + 63) / 64);
+    c.line("          const int idx = it * 64 + lane;");
+    if ((32 * chd / 4) % 64) c.line("          if (idx < %d) {", 32 * chd / 4);
+    else c.line("          {");
+    c.line("          const int r = idx / %d, e = idx - r * %d;", chd / 4, chd / 4);
+    c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
+    c.line("          const float4 v = xg[(i64)rr * %d + e];", s.in1 / 4);
+    c.line("          real* dst = &xs[wave][r][e * 4];");
+    c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
+    c.line("          }");
+    c.line("        }");
+    // Weights W_p[c0 .. c0+15, w0 .. w0+63], zero past mul3.
+    if (wvec) {
+      c.line("        #pragma unroll");
+      c.line("        for (int it = 0; it < %d; ++it) {", kStageU * 16 / 64);
+      c.line("          const int idx = it * 64 + lane, kk = idx >> 4, w4 = (idx & 15) * 4;");
+      c.line("          float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);");
+      c.line("          if (w0 + w4 < %d) v = *(const float4*)(wt + %d + (i64)(c0 + kk) * %d + w0 + w4);", mul3,
+             q.w_off, mul3);
+      c.line("          *(float4*)&ws[wave][kk][w4] = v;");
+      c.line("        }");
+    } else {
+      c.line("        #pragma unroll");
+      c.line("        for (int it = 0; it < %d; ++it) {", kStageU);
+      c.line("          const int w = w0 + lane;");
+      c.line("          ws[wave][it][lane] = w < %d ? wt[%d + (i64)(c0 + it) * %d + w] : 0.0f;", mul3, q.w_off,
+             mul3);
+      c.line("        }");
+    }
+    c.line("        }");
+    c.line("        const real* xl = &xs[wave][col][0];");
+    c.line("        #pragma unroll 2");
+    c.line("        for (int s = 0; s < %d; ++s) {", kStageU / 2);
+    c.line("          const int ul = 2 * s + hk;");
+    for (int i : is) c.line("          const real x%d = xl[ul * %d + %d];", i, q.d1, i);
+    c.line("          const real a0 = ws[wave][ul][col], a1 = ws[wave][ul][32 + col];");
+    for (int k = 0; k < d3; ++k) c.line("          real z%d = 0;", k);
+    for (const auto& t : q.terms)
+      c.line("          z%d = FMA(%s, x%d * y%d, z%d);", t.k, flit(t.c).c_str(), t.i, t.j, t.k);
+    for (int k = 0; k < d3; ++k) {
+      c.line("          acc0_%d = mfma32(a0, z%d, acc0_%d);", k, k, k);
+      c.line("          acc1_%d = mfma32(a1, z%d, acc1_%d);", k, k, k);
+    }
+    c.line("        }");
+    c.line("      }");
+    c.line("    }");
+  }
+  c.line("    if (b0 + col < B) {");
+  c.line("      real* orow = out + (i64)(b0 + col) * %d + %d;", s.out, head.out_off);
+  c.line("      #pragma unroll");
+  c.line("      for (int r = 0; r < 16; ++r) {");
+  for (int t = 0; t < 2; ++t) {
+    c.line("        {");
+    c.line("          const int w = w0 + %d + 8 * (r >> 2) + 4 * hk + (r & 3);", 32 * t);
+    c.line("          if (w < %d) {", mul3);
+    for (int k = 0; k < d3; ++k)
+      c.line("            orow[w * %d + %d] %s acc%d_%d[r];", d3, k, u.accumulate ? "+=" : "=", t, k);
+    c.line("          }");
+    c.line("        }");
+  }
+  c.line("      }");
+  c.line("    }");
+  c.line("    return;");
+  c.line("  }");
+  c.line("  unit -= %d;", nt);
+}
+
+// A dma unit (see dma_unit): as emit_forward_wide, with chunks of kDmaU
+// channels copied by global_load_lds straight into one of two LDS buffers per
+// wave while the other is used, so the next chunk streams in during the
+// current chunk's matrix work.  Lane l of copy instruction i lands 16 bytes at
+// buffer float 256 i + 4 l, so the x chunk is laid out piece-major: 4-float
+// piece `pc` of the chunk's row `row` sits at float (32 pc + row) * 4, and a
+// lane reads its row's pieces with 16-byte LDS reads, consecutive lanes on
+// consecutive slots.  The two K halves of an MFMA take channels st and st + 4
+// of the chunk, so both halves find x_i at the same place in their pieces.
+//
+// The unit's body is a function whose four buffers are __restrict__
+// arguments: inlined, every copy and every LDS read carries the alias scope of
+// its buffer, and the compiler waits before a read only for the copies into
+// that buffer (without the scopes it waits for every copy in flight).
+void emit_dma_unit_body(Code& c, const UvwSpec& s, const Unit& u) {
+  const UvwPath& head = s.paths[u.paths[0]];
+  const int d3 = head.d3, mul3 = head.mul3;
+  for (int p : u.paths) {
+    const UvwPath& q = s.paths[p];
+    const std::set<int> is = term_is(q), js = term_js(q);
+    const int d1 = q.d1, nch = q.mul1 / kDmaU;
+    c.line("  {");
+    c.line("    const real* ys = y + (i64)brow * %d + %d;", s.in2, q.y_off);
+    for (int j : js) c.line("    const real y%d = ys[%d];", j, j);
+    c.line("    const real* xrow = x + (i64)rrow * %d + %d + (lane >> 5) * 4;", s.in1, q.x_off);
+    c.line("    const real* wrow = wt + %d + (i64)(lane >> 4) * %d + wl;", q.w_off, mul3);
+    auto copy = [&](const char* chunk, const char* X, const char* W) {
+      for (int i = 0; i < d1; ++i)
+        c.line("      __builtin_amdgcn_global_load_lds((const void*)(xrow + (%s) * %d + %d), (lvoid*)(%s + %d), 16, 0, 0);",
+               chunk, kDmaU * d1, 8 * i, X, 256 * i);
+      for (int i = 0; i < 2; ++i)
+        c.line("      __builtin_amdgcn_global_load_lds((const void*)(wrow + (i64)((%s) * %d + %d) * %d), "
+               "(lvoid*)(%s + %d), 16, 0, 0);",
+               chunk, kDmaU, 4 * i, mul3, W, 256 * i);
+    };
+    // Wait until only `left` copies are in flight (vmcnt counts in issue order).
+    auto wait = [&](int left) {
+      c.line("      __builtin_amdgcn_s_waitcnt(0x0F70 | %d);", left);
+      c.line("      __builtin_amdgcn_sched_barrier(0);");
+    };
+    auto compute = [&](const char* X, const char* W) {
+      c.line("      {");
+      c.line("        const lfloat4* xp = (const lfloat4*)%s + hk * %d + col;", X, 32 * d1);
+      for (int st = 0; st < kDmaU / 2; ++st) {
+        c.line("        {");
+        std::set<int> pieces;
+        for (int i : is) pieces.insert((st * d1 + i) / 4);
+        for (int pc : pieces) c.line("          const float4 q%d = xp[%d];", pc, 32 * pc);
+        for (int i : is)
+          c.line("          const real x%d = q%d.%c;", i, (st * d1 + i) / 4, "xyzw"[(st * d1 + i) % 4]);
+        c.line("          const real a0 = %s[(%d + 4 * hk) * 64 + col], a1 = %s[(%d + 4 * hk) * 64 + 32 + col];", W, st,
+               W, st);
+        for (int k = 0; k < d3; ++k) c.line("          real z%d = 0;", k);
+        for (const auto& t : q.terms)
+          c.line("          z%d = FMA(%s, x%d * y%d, z%d);", t.k, flit(t.c).c_str(), t.i, t.j, t.k);
+        for (int k = 0; k < d3; ++k) {
+          c.line("          acc[0][%d] = mfma32(a0, z%d, acc[0][%d]);", k, k, k);
+          c.line("          acc[1][%d] = mfma32(a1, z%d, acc[1][%d]);", k, k, k);
+        }
+        c.line("        }");
+      }
+      c.line("      }");
+    };
+    const int ncopy = d1 + 2;
+    c.line("    {");
+    copy("0", "X0", "W0");
+    c.line("    }");
+    c.line("    #pragma unroll 1");
+    c.line("    for (int c = 0; c < %d; c += 2) {", nch);
+    copy("c + 1", "X1", "W1");
+    wait(ncopy);
+    compute("X0", "W0");
+    c.line("      if (c + 2 < %d) {", nch);
+    copy("c + 2", "X0", "W0");
+    wait(ncopy);
+    c.line("      } else {");
+    wait(0);
+    c.line("      }");
+    compute("X1", "W1");
+    c.line("    }");
+    c.line("  }");
+  }
+}
+
+// The unit branch inside the phase function: tiles of this unit return true
+// after storing; others move `unit` past it.
+void emit_forward_dma(Code& c, const UvwSpec& s, const Unit& u, int nt) {
+  const UvwPath& head = s.paths[u.paths[0]];
+  const int d3 = head.d3, mul3 = head.mul3;
+  c.line("  if (unit < %d) {", nt);
+  c.line("    const int w0 = unit * 64;");
+  c.line("    floatx16 acc[2][%d];", d3);
+  for (int t = 0; t < 2; ++t)
+    for (int k = 0; k < d3; ++k) c.line("    acc[%d][%d] = (floatx16)(0.0f);", t, k);
+  c.line("    const int wl = (w0 + (lane & 15) * 4 < %d) ? w0 + (lane & 15) * 4 : %d;", mul3, mul3 - 4);
+  emit_dma_unit_body(c, s, u);
+  c.line("    if (b0 + col < B) {");
+  c.line("      real* orow = out + (i64)(b0 + col) * %d + %d;", s.out, head.out_off);
+  c.line("      #pragma unroll");
+  c.line("      for (int r = 0; r < 16; ++r) {");
+  for (int t = 0; t < 2; ++t) {
+    c.line("        {");
+    c.line("          const int w = w0 + %d + 8 * (r >> 2) + 4 * hk + (r & 3);", 32 * t);
+    c.line("          if (w < %d) {", mul3);
+    for (int k = 0; k < d3; ++k)
+      c.line("            orow[w * %d + %d] %s acc[%d][%d][r];", d3, k, u.accumulate ? "+=" : "=", t, k);
+    c.line("          }");
+    c.line("        }");
+  }
+  c.line("      }");
+  c.line("    }");
+  c.line("    return true;");
+  c.line("  }");
+  c.line("  unit -= %d;", nt);
+}
+
+// Every dma unit of a phase in one function, so the four buffers carry the
+// same four alias scopes in all of them (the compiler tracks few scopes).
+void emit_forward_dma_phase(Code& c, const UvwSpec& s, const std::vector<Unit>& units, int phase) {
+  c.line("__device__ __forceinline__ bool fwd_dma_%d(int unit, const real* __restrict__ x,", phase);
+  c.line("    const real* __restrict__ y, const real* __restrict__ wt, real* __restrict__ out, int B, int b0,");
+  c.line("    int brow, int hk, int col, int lane, lreal* __restrict__ X0, lreal* __restrict__ X1,");
+  c.line("    lreal* __restrict__ W0, lreal* __restrict__ W1) {");
+  c.line("  const int rrow = b0 + col < B ? b0 + col : B - 1;");
+  for (const Unit& u : units) {
+    if (u.phase != phase) continue;
+    if (dma_unit(s, u)) emit_forward_dma(c, s, u, fwd_tiles(s, u));
+    else c.line("  unit -= %d;", fwd_tiles(s, u));
+  }
+  c.line("  return false;");
+  c.line("}");
+}
+
 std::string emit_forward(const UvwSpec& s, const std::vector<Unit>& units, int phases) {
   Code c;
   c.s << kPrelude;
   for (int phase = 0; phase < phases; ++phase) {
-    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_fwd_p%d(", phase);
+    {
+      bool any = false;
+      for (const Unit& u : units) any = any || (u.phase == phase && dma_unit(s, u));
+      if (any) emit_forward_dma_phase(c, s, units, phase);
+    }
+    bool wide_phase = false;
+    for (const Unit& u : units)
+      if (u.phase == phase && wide_unit(s, u)) wide_phase = true;
+    // Two waves per SIMD for the wide units' 32 d3 accumulator registers.
+    c.line("extern \"C\" __global__ void __launch_bounds__(256) %sluna_uvw_fwd_p%d(",
+           wide_phase ? "__attribute__((amdgpu_waves_per_eu(2))) " : "", phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    real* __restrict__ out, int B) {");
     emit_head(c);
@@ -268,18 +539,44 @@ std::string emit_forward(const UvwSpec& s, const std::vector<Unit>& units, int p
     for (const Unit& u : units)
       if (u.phase == phase)
         for (int p : u.paths)
-          if (staged_path(s, s.paths[p])) stage_d1 = std::max(stage_d1, s.paths[p].d1);
+          if (staged_path(s, s.paths[p]) && !dma_unit(s, u)) stage_d1 = std::max(stage_d1, s.paths[p].d1);
+    bool any_wide = false;
+    for (const Unit& u : units)
+      if (u.phase == phase && wide_unit(s, u) && !dma_unit(s, u)) any_wide = true;
     // Row pitch kStageU*d1 + 1: the 32 rows read at one offset fall in 32 banks.
     if (stage_d1) c.line("  __shared__ real xs[4][32][%d];", kStageU * stage_d1 + 1);
+    int dma_d1 = 0;
+    for (const Unit& u : units)
+      if (u.phase == phase && dma_unit(s, u))
+        for (int p : u.paths) dma_d1 = std::max(dma_d1, s.paths[p].d1);
+    if (any_wide) c.line("  __shared__ __attribute__((aligned(16))) real ws[4][%d][64];", kStageU);
+    if (dma_d1) {
+      // One array, so the two buffers are laid out back to back.
+      c.line("  __shared__ __attribute__((aligned(16))) real xwd[4][2][%d];", 32 * kDmaU * dma_d1 + kDmaU * 64);
+    }
     c.line("  const int b0 = (blockIdx.x * 4 + wave) * 32;");
     c.line("  if (b0 >= B) return;");
     c.line("  const int brow = b0 + col < B ? b0 + col : B - 1;");
+    if (dma_d1) {
+      const int woff = 32 * kDmaU * dma_d1;
+      c.line("  if (fwd_dma_%d(blockIdx.y, x, y, wt, out, B, b0, brow, hk, col, lane, (lreal*)&xwd[wave][0][0],", phase);
+      c.line("      (lreal*)&xwd[wave][1][0], (lreal*)&xwd[wave][0][%d], (lreal*)&xwd[wave][1][%d])) return;", woff, woff);
+    }
     c.line("  int unit = blockIdx.y;");
-    for (const Unit& u : units) {
+    for (size_t n = 0; n < units.size(); ++n) {
+      const Unit& u = units[n];
       if (u.phase != phase) continue;
       const UvwPath& head = s.paths[u.paths[0]];
       const int d3 = head.d3, mul3 = head.mul3;
-      const int nt = (mul3 + 31) / 32;
+      const int nt = fwd_tiles(s, u);
+      if (dma_unit(s, u)) {
+        c.line("  unit -= %d;", nt);
+        continue;
+      }
+      if (wide_unit(s, u)) {
+        emit_forward_wide(c, s, u, nt);
+        continue;
+      }
       c.line("  if (unit < %d) {", nt);
       c.line("    const int w0 = unit * 32;");
       for (int k = 0; k < d3; ++k) c.line("    floatx16 acc%d = (floatx16)(0.0f);", k);
@@ -394,7 +691,26 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 }
 )";
   for (int phase = 0; phase < phases; ++phase) {
-    c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_xy_p%d(", phase);
+    // Four waves per SIMD when the per-lane state is small: short waves whose
+    // staging latency is hidden by occupancy (1.29 -> 1.09 ms at 64x0e+64x1o+64x2e);
+    // the estimate counts x and gx entries (4 K rows of d1), dZ (4 d3) and the
+    // gy columns, plus addresses and staging temporaries.
+    bool four = true;
+    for (const Unit& un : units) {
+      if (un.phase != phase) continue;
+      const UvwPath& head = s.paths[un.paths[0]];
+      int d3 = 0;
+      std::set<int> ycols;
+      for (int p : un.paths) {
+        d3 = std::max(d3, s.paths[p].d3);
+        for (int v = 0; v < s.paths[p].mul2; ++v)
+          for (int j : term_js(s.paths[p])) ycols.insert(s.paths[p].y_off + v * s.paths[p].d2 + j);
+      }
+      const int estimate = 8 * head.d1 + 4 * d3 + 2 * (int)ycols.size() + 48;
+      if (estimate > 128) four = false;
+    }
+    c.line("extern \"C\" __global__ void __launch_bounds__(256) %sluna_uvw_bwd_xy_p%d(",
+           four ? "__attribute__((amdgpu_waves_per_eu(4))) " : "", phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B) {");
     c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
@@ -597,7 +913,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 // seed rows (columns w), contraction over (b, k) two batch rows per
 // instruction and one instruction per k.  Each wave owns kChunkRows rows of
 // one path and writes one partial of dW_p; a second kernel sums the partials.
-std::string emit_backward_w(const UvwSpec& s) {
+std::string emit_backward_w(const UvwSpec& s, int chunk_rows) {
   Code c;
   c.s << kPrelude;
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w(");
@@ -605,7 +921,7 @@ std::string emit_backward_w(const UvwSpec& s) {
   c.line("    real* __restrict__ part, int B) {");
   emit_head(c);
   c.line("  const int chunk = blockIdx.x * 4 + wave;");
-  c.line("  const int r0 = chunk * %d;", kChunkRows);
+  c.line("  const int r0 = chunk * %d;", chunk_rows);
   c.line("  if (r0 >= B) return;");
   c.line("  const int path = blockIdx.y;");
   for (int p = 0; p < (int)s.paths.size(); ++p) {
@@ -626,7 +942,7 @@ std::string emit_backward_w(const UvwSpec& s) {
       c.line("    const bool wok%d = w%d < %d;", n, n, q.mul3);
     }
     c.line("    #pragma unroll 2");
-    c.line("    for (int s = 0; s < %d; ++s) {", kChunkRows / 2);
+    c.line("    for (int s = 0; s < %d; ++s) {", chunk_rows / 2);
     c.line("      const int row = r0 + 2 * s + hk;");
     c.line("      const bool rok = row < B;");
     c.line("      const int rc = rok ? row : B - 1;");
@@ -710,13 +1026,14 @@ struct UvwPlan {
   int fwd_phases = 0, bwd_phases = 0;
   std::vector<int> fwd_phase_tiles, bwd_phase_tiles;  // grid.y per phase
   int gy_slots = 0;
+  int chunk_rows = kChunkRows;
   bool out_needs_zero = false, gx_needs_zero = false, gy_needs_zero = false, gw_needs_zero = false;
 };
 
 std::string source_for(const UvwPlan& plan, const std::string& variant) {
   if (variant == "fwd") return emit_forward(plan.spec, plan.fwd_units, plan.fwd_phases);
   if (variant == "bxy") return emit_backward_xy(plan.spec, plan.bwd_units, plan.bwd_phases);
-  return emit_backward_w(plan.spec);
+  return emit_backward_w(plan.spec, plan.chunk_rows);
 }
 
 bool covers(const std::vector<std::pair<long, long>>& ranges, long total) {
@@ -745,11 +1062,11 @@ hipModule_t module_for(UvwPlan& plan, const std::string& variant) {
   return plan.kernels.module_for(variant, [&] { return source_for(plan, variant); });
 }
 
-int64_t chunks_for(int64_t rows) { return (rows + kChunkRows - 1) / kChunkRows; }
+int64_t chunks_for(const UvwPlan& p, int64_t rows) { return (rows + p.chunk_rows - 1) / p.chunk_rows; }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 size_t gw_part_bytes(const UvwPlan& p, int64_t rows) {
-  return align256((size_t)chunks_for(rows) * (size_t)p.spec.wnum * sizeof(float)) +
+  return align256((size_t)chunks_for(p, rows) * (size_t)p.spec.wnum * sizeof(float)) +
          align256((size_t)kReduceGroups * (size_t)p.spec.wnum * sizeof(float));
 }
 size_t gy_part_bytes(const UvwPlan& p, int64_t rows) {
@@ -769,6 +1086,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     auto holder = std::make_unique<LunaUvwPlan>();
     UvwPlan& p = holder->plan;
     p.spec = parse(spec);
+
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
     p.kernels.tag = "uvw";
     std::vector<std::pair<long, long>> xs, ws;
@@ -782,7 +1100,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.fwd_phase_tiles.assign(p.fwd_phases, 0);
     std::vector<std::pair<long, long>> outs;
     for (const Unit& u : p.fwd_units) {
-      p.fwd_phase_tiles[u.phase] += (p.spec.paths[u.paths[0]].mul3 + 31) / 32;
+      p.fwd_phase_tiles[u.phase] += fwd_tiles(p.spec, u);
       outs.push_back({u.lo, u.hi});
     }
     p.bwd_units = backward_units(p.spec);
@@ -883,7 +1201,7 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
     }
     if (gw) {
       hipModule_t module = module_for(plan, "bw");
-      const int64_t chunks = chunks_for(rows);
+      const int64_t chunks = chunks_for(plan, rows);
       if (rows > 0) {
         void* args[] = {&x, &y, &g, &gw_part, &B};
         launch("uvw_bwd_w", function_for(module, "luna_uvw_bwd_w"),
