@@ -171,7 +171,8 @@ int luna_uvw_bwd_workspace(const LunaUvwPlan* plan, int64_t rows, size_t* bytes)
 /*
  * Backward of luna_uvw_fwd for seed g [rows, out]: gx and gy (both or neither)
  * and gw [weight_numel] (NULL to skip).  workspace must hold
- * luna_uvw_bwd_workspace bytes whenever anything is requested.
+ * luna_uvw_bwd_workspace bytes whenever anything is requested.  With rows == 0
+ * x, y and g may be NULL; gw is then written as zeros.
  * replaces: the UVW backward launcher (src/lunatp/uvw/interface.py:42-49)
  */
 int luna_uvw_bwd(const LunaUvwPlan* plan, const void* x, const void* y, const void* weight,

@@ -1177,7 +1177,8 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
   return guard_call([&] {
     if (!cplan) fail("luna_uvw_bwd: null plan");
     if (rows < 0 || rows > 0x7fffffffLL) fail("luna_uvw_bwd: bad row count");
-    if (!x || !y || !weight || !g) fail("luna_uvw_bwd: null tensor");
+    // An empty batch may come with null row tensors (gw is then zero).
+    if (!weight || (rows > 0 && (!x || !y || !g))) fail("luna_uvw_bwd: null tensor");
     UvwPlan& plan = const_cast<LunaUvwPlan*>(cplan)->plan;
     hipStream_t s = (hipStream_t)stream;
     int B = (int)rows;

@@ -112,3 +112,28 @@ def test_uvw_module_dtype_switch():
     y = torch.randn(20, tp.irreps_in2.dim, device=DEV, dtype=torch.float64)
     ref = uvw_tensor_product(ir, sh, ir, instructions, x.cpu(), y.cpu(), tp.weight.detach().cpu())
     assert_close(tp(x, y), ref, torch.float64, "fp64 after .double()")
+
+
+@pytest.mark.parametrize("rows", [0, 1, 45])
+def test_uvw_degree3_and_tiny_batches(rows):
+    """Output blocks of degree 3 (seven components: 32-channel tiles) beside 64-wide
+    units, on an empty batch, a single row and a ragged one."""
+    in1, in2, out = "64x0e+32x1o", "1x0e+1x1o+1x2e", "64x0e+64x1o+32x3o"
+    instructions = uvw_instructions(in1, in2, out)
+    tp = lunaeq.TensorProduct(in1, in2, out, instructions, shared_weights=True, internal_weights=False)
+    gen = torch.Generator().manual_seed(7 + rows)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64) / 8
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ref = uvw_tensor_product(in1, in2, out, instructions, *ref_in)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in)
+    assert act.shape == (rows, tp.irreps_out.dim)
+    assert_close(act, ref, torch.float32, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    ref_first = torch.autograd.grad(ref, ref_in, g)
+    dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32))
+    for n, (a, r) in enumerate(zip(dev_first, ref_first)):
+        assert a.shape == r.shape
+        assert_close(a, r, torch.float32, f"first-order {n}")
