@@ -94,3 +94,29 @@ def test_uuu_batch_broadcasting():
     assert out.shape == (4, 3, 8)
     expected = (x.reshape(4, 1, 8, 3) * y.reshape(1, 3, 8, 3)).sum(-1) * w / 3 ** 0.5
     assert_close(out, expected.double(), torch.float32, "broadcast")
+
+
+@pytest.mark.parametrize("rows", [0, 1])
+@pytest.mark.parametrize("mode", ["uvu", "uuu"])
+def test_rowwise_tiny_batches(mode, rows):
+    """No rows and one row, shared weights: outputs and first-order gradients."""
+    in1, in2, out = CASES[mode]
+    ins = paths(mode, in1, in2, out)
+    tp = lunaeq.TensorProduct(in1, in2, out, ins, shared_weights=True, internal_weights=False)
+    gen = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64)
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ids = torch.arange(rows)
+    ref = oracle_conv(in1, in2, out, ins, ref_in[0], ref_in[1], ref_in[2].expand(rows, -1), ids, ids, rows)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in)
+    assert act.shape == (rows, tp.irreps_out.dim)
+    assert_close(act, ref, torch.float32, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    ref_first = torch.autograd.grad(ref, ref_in, g)
+    dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32))
+    for n, (a, r) in enumerate(zip(dev_first, ref_first)):
+        assert a.shape == r.shape
+        assert_close(a, r, torch.float32, f"first-order {n}")
