@@ -267,6 +267,14 @@ std::set<int> term_js(const UvwPath& q) {
   return r;
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// the wave are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt
+// and lgkmcnt left at their maxima, i.e. not waited for).
+int vmcnt_imm(int n) {
+  if (n < 0 || n > 63) fail("uvw: vmcnt out of range");
+  return 0x0F70 | (n & 15) | ((n >> 4) << 14);
+}
+
 const char* kPrelude = R"(
 typedef float real;
 typedef long long i64;
@@ -421,7 +429,7 @@ void emit_dma_unit_body(Code& c, const UvwSpec& s, const Unit& u) {
     };
     // Wait until only `left` copies are in flight (vmcnt counts in issue order).
     auto wait = [&](int left) {
-      c.line("      __builtin_amdgcn_s_waitcnt(0x0F70 | %d);", left);
+      c.line("      __builtin_amdgcn_s_waitcnt(%d);", vmcnt_imm(left));
       c.line("      __builtin_amdgcn_sched_barrier(0);");
     };
     auto compute = [&](const char* X, const char* W) {
@@ -913,17 +921,164 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 // seed rows (columns w), contraction over (b, k) two batch rows per
 // instruction and one instruction per k.  Each wave owns kChunkRows rows of
 // one path and writes one partial of dW_p; a second kernel sums the partials.
+// Weight-gradient paths whose x and seed rows are copied by global_load_lds
+// into two LDS buffers per wave, kWRows rows at a time, the next rows in flight
+// during the current rows' matrix work (LUNAEQ_AMD_UVW_WDMA=0 turns this off).
+// Rows stay row-major in LDS: a lane reads x[row][u d1 + i] and
+// g[row][w d3 + k] for consecutive u or w, an odd stride, so no bank conflicts.
+constexpr int kWRows = 4;
+bool bw_dma_path(const UvwSpec& s, const UvwPath& q) {
+  const char* e = std::getenv("LUNAEQ_AMD_UVW_WDMA");
+  if (e && std::atoi(e) == 0) return false;
+  return q.mul2 == 1 && (q.mul1 * q.d1) % 4 == 0 && (q.mul3 * q.d3) % 4 == 0 && q.x_off % 4 == 0 &&
+         q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0;
+}
+int bw_pieces(int floats_per_row) { return (kWRows * floats_per_row / 4 + 63) / 64 * 64; }
+
+// All such paths in one function (four __restrict__ buffers, so the
+// compiler's waits before LDS reads cover only the copies into the buffer
+// being read).  Returns false for other paths.
+void emit_bw_dma(Code& c, const UvwSpec& s, int chunk_rows) {
+  c.line("__device__ __forceinline__ bool bw_dma(int path, const real* __restrict__ x, const real* __restrict__ y,");
+  c.line("    const real* __restrict__ g, real* __restrict__ part, int B, int chunk, int r0, int lane, int col,");
+  c.line("    int hk, lreal* __restrict__ X0, lreal* __restrict__ X1, lreal* __restrict__ G0,");
+  c.line("    lreal* __restrict__ G1, lreal* __restrict__ Y0, lreal* __restrict__ Y1) {");
+  for (int p = 0; p < (int)s.paths.size(); ++p) {
+    const UvwPath& q = s.paths[p];
+    if (!bw_dma_path(s, q)) continue;
+    const int K = q.mul1, mt = ktiles(q), nt = (q.mul3 + 31) / 32, d3 = q.d3, d1 = q.d1;
+    const int px = q.mul1 * d1, pg = q.mul3 * d3;  // floats per row of the x block and of the seed block
+    const int nx = bw_pieces(px) / 64, ng = bw_pieces(pg) / 64, ncopy = nx + ng + 1;
+    const int d2 = q.d2;
+    const int nch = chunk_rows / kWRows;
+    const std::set<int> is = term_is(q), js = term_js(q);
+    c.line("  if (path == %d) {", p);
+    for (int m = 0; m < mt; ++m)
+      for (int n = 0; n < nt; ++n) c.line("    floatx16 acc%d_%d = (floatx16)(0.0f);", m, n);
+    for (int m = 0; m < mt; ++m) {
+      c.line("    const bool kok%d = %d + col < %d;", m, m * 32, K);
+      c.line("    const int xu%d = (kok%d ? %d + col : %d) * %d;", m, m, m * 32, K - 1, d1);
+    }
+    for (int n = 0; n < nt; ++n) {
+      c.line("    const bool wok%d = %d + col < %d;", n, n * 32, q.mul3);
+      c.line("    const int gw%d = (wok%d ? %d + col : %d) * %d;", n, n, n * 32, q.mul3 - 1, d3);
+    }
+    // Copy instruction i, lane l: 16-byte piece 64 i + l of the rows, row-major
+    // (pieces past the rows re-read the last piece into the buffer's tail).
+    for (int i = 0; i < nx; ++i) {
+      c.line("    const int xpc%d = 64 * %d + lane < %d ? 64 * %d + lane : %d;", i, i, kWRows * px / 4, i,
+             kWRows * px / 4 - 1);
+      c.line("    const int xrow%d = xpc%d / %d, xoff%d = %d + (xpc%d - xrow%d * %d) * 4;", i, i, px / 4, i, q.x_off, i, i,
+             px / 4);
+    }
+    for (int i = 0; i < ng; ++i) {
+      c.line("    const int gpc%d = 64 * %d + lane < %d ? 64 * %d + lane : %d;", i, i, kWRows * pg / 4, i,
+             kWRows * pg / 4 - 1);
+      c.line("    const int grow%d = gpc%d / %d, goff%d = %d + (gpc%d - grow%d * %d) * 4;", i, i, pg / 4, i, q.out_off, i,
+             i, pg / 4);
+    }
+    // y: one 4-byte copy per lane, lane l = (row l / d2, column l % d2).
+    c.line("    const int yl = lane < %d ? lane : %d;", kWRows * d2, kWRows * d2 - 1);
+    c.line("    const int yrow = yl / %d, ycol = %d + yl - yrow * %d;", d2, q.y_off, d2);
+    auto copy = [&](const char* cb, const char* X, const char* G, const char* Y) {
+      for (int i = 0; i < nx; ++i)
+        c.line("      __builtin_amdgcn_global_load_lds((const void*)(x + (i64)min(%s + xrow%d, B - 1) * %d + xoff%d), "
+               "(lvoid*)(%s + %d), 16, 0, 0);", cb, i, s.in1, i, X, 256 * i);
+      for (int i = 0; i < ng; ++i)
+        c.line("      __builtin_amdgcn_global_load_lds((const void*)(g + (i64)min(%s + grow%d, B - 1) * %d + goff%d), "
+               "(lvoid*)(%s + %d), 16, 0, 0);", cb, i, s.out, i, G, 256 * i);
+      c.line("      __builtin_amdgcn_global_load_lds((const void*)(y + (i64)min(%s + yrow, B - 1) * %d + ycol), "
+             "(lvoid*)%s, 4, 0, 0);", cb, s.in2, Y);
+    };
+    auto wait = [&](int left) {
+      c.line("      __builtin_amdgcn_s_waitcnt(%d);", vmcnt_imm(left));
+      c.line("      __builtin_amdgcn_sched_barrier(0);");
+    };
+    auto compute = [&](const char* cb, const char* X, const char* G, const char* Y) {
+      for (int sp = 0; sp < kWRows / 2; ++sp) {
+        c.line("      {");
+        c.line("        const bool rok = %s + %d + hk < B;", cb, 2 * sp);
+        for (int j : js) c.line("        const real y%d_%d = %s[(%d + hk) * %d + %d];", sp, j, Y, 2 * sp, d2, j);
+        c.line("        const lreal* xl = %s + (%d + hk) * %d;", X, 2 * sp, px);
+        c.line("        const lreal* gl = %s + (%d + hk) * %d;", G, 2 * sp, pg);
+        for (int m = 0; m < mt; ++m) {
+          for (int i : is) c.line("        const real x%d_%d = xl[xu%d + %d];", m, i, m, i);
+          for (int k = 0; k < d3; ++k) c.line("        real z%d_%d = 0;", m, k);
+          for (const auto& t : q.terms)
+            c.line("        z%d_%d = FMA(%s, x%d_%d * y%d_%d, z%d_%d);", m, t.k, flit(t.c).c_str(), m, t.i, sp, t.j, m,
+                   t.k);
+          for (int k = 0; k < d3; ++k) c.line("        z%d_%d = (rok && kok%d) ? z%d_%d : 0.0f;", m, k, m, m, k);
+        }
+        for (int n = 0; n < nt; ++n)
+          for (int k = 0; k < d3; ++k) c.line("        const real g%d_%d = wok%d ? gl[gw%d + %d] : 0.0f;", n, k, n, n, k);
+        for (int k = 0; k < d3; ++k)
+          for (int m = 0; m < mt; ++m)
+            for (int n = 0; n < nt; ++n)
+              c.line("        acc%d_%d = mfma32(z%d_%d, g%d_%d, acc%d_%d);", m, n, m, k, n, k, m, n);
+        c.line("      }");
+      }
+    };
+    c.line("    {");
+    copy("r0", "X0", "G0", "Y0");
+    c.line("    }");
+    c.line("    #pragma unroll 1");
+    c.line("    for (int cc = 0; cc < %d; cc += 2) {", nch);
+    c.line("      const int ca = r0 + cc * %d, cb = ca + %d;", kWRows, kWRows);
+    copy("cb", "X1", "G1", "Y1");
+    wait(ncopy);
+    compute("ca", "X0", "G0", "Y0");
+    c.line("      if (cc + 2 < %d) {", nch);
+    const std::string next = "cb + " + std::to_string(kWRows);
+    copy(next.c_str(), "X0", "G0", "Y0");
+    wait(ncopy);
+    c.line("      } else {");
+    wait(0);
+    c.line("      }");
+    compute("cb", "X1", "G1", "Y1");
+    c.line("    }");
+    // Register r: K = 32 m + 8(r/4) + 4hk + r%4, w = 32 n + col.
+    c.line("    real* pr = part + (i64)chunk * %d + %d;", s.wnum, q.w_off);
+    for (int m = 0; m < mt; ++m)
+      for (int n = 0; n < nt; ++n) {
+        c.line("    if (wok%d) {", n);
+        c.line("      #pragma unroll");
+        c.line("      for (int r = 0; r < 16; ++r) {");
+        c.line("        const int kr = %d + 8 * (r >> 2) + 4 * hk + (r & 3);", m * 32);
+        c.line("        if (kr < %d) pr[(i64)kr * %d + %d + col] = acc%d_%d[r];", K, q.mul3, 32 * n, m, n);
+        c.line("      }");
+        c.line("    }");
+      }
+    c.line("    return true;");
+    c.line("  }");
+  }
+  c.line("  return false;");
+  c.line("}");
+}
+
 std::string emit_backward_w(const UvwSpec& s, int chunk_rows) {
   Code c;
   c.s << kPrelude;
+  int xmax = 0, gmax = 0;
+  for (const auto& q : s.paths)
+    if (bw_dma_path(s, q)) {
+      xmax = std::max(xmax, bw_pieces(q.mul1 * q.d1) * 4);
+      gmax = std::max(gmax, bw_pieces(q.mul3 * q.d3) * 4);
+    }
+  if (xmax) emit_bw_dma(c, s, chunk_rows);
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w(");
   c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ g,");
   c.line("    real* __restrict__ part, int B) {");
+  if (xmax) c.line("  __shared__ __attribute__((aligned(16))) real buf[4][2][%d];", xmax + gmax + 64);
   emit_head(c);
   c.line("  const int chunk = blockIdx.x * 4 + wave;");
   c.line("  const int r0 = chunk * %d;", chunk_rows);
   c.line("  if (r0 >= B) return;");
   c.line("  const int path = blockIdx.y;");
+  if (xmax) {
+    c.line("  if (bw_dma(path, x, y, g, part, B, chunk, r0, lane, col, hk, (lreal*)&buf[wave][0][0],");
+    c.line("             (lreal*)&buf[wave][1][0], (lreal*)&buf[wave][0][%d], (lreal*)&buf[wave][1][%d],", xmax, xmax);
+    c.line("             (lreal*)&buf[wave][0][%d], (lreal*)&buf[wave][1][%d])) return;", xmax + gmax, xmax + gmax);
+  }
   for (int p = 0; p < (int)s.paths.size(); ++p) {
     const UvwPath& q = s.paths[p];
     const int K = q.mul1 * q.mul2, mt = ktiles(q), nt = (q.mul3 + 31) / 32, d3 = q.d3;
