@@ -921,19 +921,24 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 // seed rows (columns w), contraction over (b, k) two batch rows per
 // instruction and one instruction per k.  Each wave owns kChunkRows rows of
 // one path and writes one partial of dW_p; a second kernel sums the partials.
-// Weight-gradient paths whose x and seed rows are copied by global_load_lds
+// Weight-gradient paths whose x, seed and y rows are copied by global_load_lds
 // into two LDS buffers per wave, kWRows rows at a time, the next rows in flight
 // during the current rows' matrix work (LUNAEQ_AMD_UVW_WDMA=0 turns this off).
 // Rows stay row-major in LDS: a lane reads x[row][u d1 + i] and
 // g[row][w d3 + k] for consecutive u or w, an odd stride, so no bank conflicts.
 constexpr int kWRows = 4;
+int bw_pieces(int floats_per_row) { return (kWRows * floats_per_row / 4 + 63) / 64 * 64; }
+// LDS of a workgroup (four waves, two buffers of x, seed and y rows) for one path.
+int bw_lds_bytes(const UvwPath& q) {
+  return 4 * 2 * (bw_pieces(q.mul1 * q.d1) * 4 + bw_pieces(q.mul3 * q.d3) * 4 + 64) * 4;
+}
 bool bw_dma_path(const UvwSpec& s, const UvwPath& q) {
   const char* e = std::getenv("LUNAEQ_AMD_UVW_WDMA");
   if (e && std::atoi(e) == 0) return false;
   return q.mul2 == 1 && (q.mul1 * q.d1) % 4 == 0 && (q.mul3 * q.d3) % 4 == 0 && q.x_off % 4 == 0 &&
-         q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0;
+         q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0 && q.d2 * kWRows <= 64 &&
+         bw_lds_bytes(q) <= 128 * 1024;
 }
-int bw_pieces(int floats_per_row) { return (kWRows * floats_per_row / 4 + 63) / 64 * 64; }
 
 // All such paths in one function (four __restrict__ buffers, so the
 // compiler's waits before LDS reads cover only the copies into the buffer

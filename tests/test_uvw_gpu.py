@@ -137,3 +137,26 @@ def test_uvw_degree3_and_tiny_batches(rows):
     for n, (a, r) in enumerate(zip(dev_first, ref_first)):
         assert a.shape == r.shape
         assert_close(a, r, torch.float32, f"first-order {n}")
+
+
+def test_uvw_wide_blocks():
+    """128- and 64-channel blocks with degree-3 components: large LDS-copied rows
+    in the weight gradient next to 32-channel forward tiles."""
+    in1, in2, out = "128x0e+64x3o", "1x0e+1x3o", "128x0e+64x3o"
+    instructions = uvw_instructions(in1, in2, out)
+    tp = lunaeq.TensorProduct(in1, in2, out, instructions, shared_weights=True, internal_weights=False)
+    rows = 300
+    gen = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64) / 16
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ref = uvw_tensor_product(in1, in2, out, instructions, *ref_in)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in)
+    assert_close(act, ref, torch.float32, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    ref_first = torch.autograd.grad(ref, ref_in, g)
+    dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32))
+    for n, (a, r) in enumerate(zip(dev_first, ref_first)):
+        assert_close(a, r, torch.float32, f"first-order {n}")
