@@ -551,17 +551,22 @@ std::string emit_forward(const UvwSpec& s, const std::vector<Unit>& units, int p
     bool any_wide = false;
     for (const Unit& u : units)
       if (u.phase == phase && wide_unit(s, u) && !dma_unit(s, u)) any_wide = true;
-    // Row pitch kStageU*d1 + 1: the 32 rows read at one offset fall in 32 banks.
-    if (stage_d1) c.line("  __shared__ real xs[4][32][%d];", kStageU * stage_d1 + 1);
     int dma_d1 = 0;
     for (const Unit& u : units)
       if (u.phase == phase && dma_unit(s, u))
         for (int p : u.paths) dma_d1 = std::max(dma_d1, s.paths[p].d1);
-    if (any_wide) c.line("  __shared__ __attribute__((aligned(16))) real ws[4][%d][64];", kStageU);
-    if (dma_d1) {
-      // One array, so the two buffers are laid out back to back.
-      c.line("  __shared__ __attribute__((aligned(16))) real xwd[4][2][%d];", 32 * kDmaU * dma_d1 + kDmaU * 64);
-    }
+    // A workgroup runs one unit, so the staging arrays of the different unit
+    // kinds share one LDS allocation: xs (row pitch kStageU*d1 + 1, so the 32
+    // rows read at one offset fall in 32 banks) and ws of the register-staged
+    // units, xwd (two buffers back to back) of the LDS-copied ones.
+    const int xs_floats = stage_d1 ? 4 * 32 * (kStageU * stage_d1 + 1) : 0;
+    const int ws_floats = any_wide ? 4 * kStageU * 64 : 0;
+    const int xwd_pitch = 32 * kDmaU * dma_d1 + kDmaU * 64;
+    const int lds_floats = std::max(round_up(xs_floats, 4) + ws_floats, dma_d1 ? 4 * 2 * xwd_pitch : 0);
+    if (lds_floats) c.line("  __shared__ __attribute__((aligned(16))) real lds[%d];", lds_floats);
+    if (stage_d1) c.line("  real (*xs)[32][%d] = (real (*)[32][%d])lds;", kStageU * stage_d1 + 1, kStageU * stage_d1 + 1);
+    if (any_wide) c.line("  real (*ws)[%d][64] = (real (*)[%d][64])(lds + %d);", kStageU, kStageU, round_up(xs_floats, 4));
+    if (dma_d1) c.line("  real (*xwd)[2][%d] = (real (*)[2][%d])lds;", xwd_pitch, xwd_pitch);
     c.line("  const int b0 = (blockIdx.x * 4 + wave) * 32;");
     c.line("  if (b0 >= B) return;");
     c.line("  const int brow = b0 + col < B ? b0 + col : B - 1;");
