@@ -812,28 +812,55 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
           // consecutive lanes on consecutive addresses; within a chunk lane
           // group grp takes w = 4 ss + grp.
           const int gw = 16 * d3;  // floats of one batch row per chunk
+          const int total = 16 * gw / 4, per = (total + 255) / 256;
+          // Chunk `cc` of the seeds (float4 pieces idx = threadIdx.x + 256 it)
+          // and of this wave's W rows into registers.
+          auto load = [&](const char* cc) {
+            for (int it = 0; it < per; ++it) {
+              c.line("        {");
+              c.line("          const int idx = threadIdx.x + %d;", 256 * it);
+              c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
+              c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
+              c.line("          if (idx < %d) pg%d = *(const float4*)(g + %d + (%s) * %d + (i64)rr * %d + e * 4);", total, it,
+                     q.out_off, cc, 16 * d3, s.out);
+              c.line("        }");
+            }
+            c.line("        {");
+            c.line("          const int r = lane >> 2, e = lane & 3, kr = kt * 16 + r;");
+            c.line("          pw = kr < %d ? *(const float4*)(wt + %d + (i64)kr * %d + (%s) * 16 + e * 4)"
+                   " : make_float4(0.0f, 0.0f, 0.0f, 0.0f);", Ktot, q.w_off, mul3, cc);
+            c.line("        }");
+          };
+          auto store = [&]() {
+            c.line("        real (*gsb)[%d] = gs[chunk & 1];", 16 * stage_d3 + 1);
+            for (int it = 0; it < per; ++it) {
+              c.line("        {");
+              c.line("          const int idx = threadIdx.x + %d;", 256 * it);
+              c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
+              c.line("          if (idx < %d) {", total);
+              c.line("            real* dst = &gsb[r][e * 4];");
+              c.line("            dst[0] = pg%d.x; dst[1] = pg%d.y; dst[2] = pg%d.z; dst[3] = pg%d.w;", it, it, it, it);
+              c.line("          }");
+              c.line("        }");
+            }
+            c.line("        {");
+            c.line("          const int r = lane >> 2, e = lane & 3;");
+            c.line("          real* dst = &wsh[wave][r][e * 4];");
+            c.line("          dst[0] = pw.x; dst[1] = pw.y; dst[2] = pw.z; dst[3] = pw.w;");
+            c.line("        }");
+          };
+          for (int it = 0; it < per; ++it) c.line("      float4 pg%d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);", it);
+          c.line("      float4 pw;");
+          // Requesting the next chunk before this chunk's matrix work (fenced
+          // with sched_barrier) measured the same and spilled registers.
           c.line("      #pragma unroll 1");
-          c.line("      for (int c0 = 0; c0 < %d; c0 += 16) {", mul3);
-          c.line("        const float4* gg = (const float4*)(g + %d + c0 * %d);", q.out_off, d3);
-          c.line("        real (*gsb)[%d] = gs[chunk & 1];", 16 * stage_d3 + 1);
-          c.line("        for (int idx = threadIdx.x; idx < %d; idx += 256) {", 16 * gw / 4);
-          c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
-          c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
-          c.line("          const float4 v = gg[(i64)rr * %d + e];", s.out / 4);
-          c.line("          real* dst = &gsb[r][e * 4];");
-          c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
-          c.line("        }");
-          c.line("        {");
-          c.line("          const int r = lane >> 2, e = lane & 3, kr = kt * 16 + r;");
-          c.line("          const float4 v = kr < %d ? *(const float4*)(wt + %d + (i64)kr * %d + c0 + e * 4)"
-                 " : make_float4(0.0f, 0.0f, 0.0f, 0.0f);", Ktot, q.w_off, mul3);
-          c.line("          real* dst = &wsh[wave][r][e * 4];");
-          c.line("          dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;");
-          c.line("        }");
+          c.line("      for (int cn = 0; cn < %d; ++cn) {", mul3 / 16);
+          load("cn");
+          store();
           c.line("        __syncthreads();");
-          c.line("        ++chunk;");
-          c.line("        const real* gl = &gsb[c16][0];");
+          c.line("        const real* gl = &gs[chunk & 1][c16][0];");
           c.line("        const real* al = &wsh[wave][c16][0];");
+          c.line("        ++chunk;");
           for (int ss = 0; ss < 4; ++ss) {
             c.line("        {");
             c.line("          const int wl = %d + grp;", 4 * ss);
