@@ -882,9 +882,11 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
         for (int r = 0; r < 4; ++r) {
           const int v = r % m2, qd = r / m2;
           for (const auto& t : q.terms) {
-            c.line("      gxa%d_%d = FMA(%s * y%d_%d, dz%d[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, t.k, r,
+            // c * (y dZ), not (c y) * dZ: products of a coefficient and an
+            // operand would be shared across the four K rows and kept live.
+            c.line("      gxa%d_%d = FMA(%s, y%d_%d * dz%d[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, t.k, r,
                    qd, t.i);
-            c.line("      gp%d_%d = FMA(%s * x%d_%d, dz%d[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, t.k, r, v,
+            c.line("      gp%d_%d = FMA(%s, x%d_%d * dz%d[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, t.k, r, v,
                    t.j);
           }
         }
