@@ -704,10 +704,13 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 }
 )";
   for (int phase = 0; phase < phases; ++phase) {
-    // Four waves per SIMD when the per-lane state is small: short waves whose
-    // staging latency is hidden by occupancy (1.29 -> 1.09 ms at 64x0e+64x1o+64x2e);
-    // the estimate counts x and gx entries (4 K rows of d1), dZ (4 d3) and the
-    // gy columns, plus addresses and staging temporaries.
+    // Four waves per SIMD when the per-lane state is small (short waves whose
+    // staging latency is hidden by occupancy: 1.29 -> 1.09 ms at
+    // 64x0e+64x1o+64x2e), else two (without the hint the compiler splits the
+    // file into VGPRs and AGPRs and leaves one wave per SIMD: 264 registers at
+    // 64x0e+64x1o+64x2e+64x3o, 232 with it, no spills).  The estimate counts x
+    // and gx entries (4 K rows of d1), dZ (4 d3) and the gy columns, plus
+    // addresses and staging temporaries.
     bool four = true;
     for (const Unit& un : units) {
       if (un.phase != phase) continue;
@@ -723,7 +726,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       if (estimate > 128) four = false;
     }
     c.line("extern \"C\" __global__ void __launch_bounds__(256) %sluna_uvw_bwd_xy_p%d(",
-           four ? "__attribute__((amdgpu_waves_per_eu(4))) " : "", phase);
+           four ? "__attribute__((amdgpu_waves_per_eu(4))) " : "__attribute__((amdgpu_waves_per_eu(2))) ", phase);
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B) {");
     c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
