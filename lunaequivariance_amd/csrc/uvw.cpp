@@ -39,6 +39,15 @@ struct UvwSpec {
   int dtype_bits = 32;
   int in1 = 0, in2 = 0, out = 0, wnum = 0;
   std::vector<UvwPath> paths;
+  // Kernel variants, fixed when the plan is created (launch geometry depends
+  // on them), from LUNAEQ_AMD_UVW_VEC (0: no 16-byte row loads),
+  // LUNAEQ_AMD_UVW_WIDE (0: 32-channel forward tiles only, 1: 64-channel tiles
+  // staged through registers, 2 or unset: 64-channel tiles with LDS copies)
+  // and LUNAEQ_AMD_UVW_WDMA (0: weight gradient without LDS copies), for
+  // comparisons.
+  bool vec = true;
+  int wide = 2;
+  bool wdma = true;
 };
 
 constexpr int kChunkRows = 256;  // default batch rows per wave (and per partial) of the weight gradient
@@ -198,19 +207,12 @@ std::vector<Unit> backward_units(const UvwSpec& s) {
 
 int ktiles(const UvwPath& q) { return (q.mul1 * q.mul2 + 31) / 32; }
 
-// 16-byte loads along a lane's own row where the layout allows
-// (LUNAEQ_AMD_UVW_VEC=0 turns them off, for comparison).
-bool vector_loads() {
-  const char* e = std::getenv("LUNAEQ_AMD_UVW_VEC");
-  return !e || std::atoi(e) != 0;
-}
-
 constexpr int kStageU = 16;  // channels u per LDS chunk of the forward's x staging
 
 // Forward paths whose x block is staged through LDS (16-byte aligned rows,
 // whole chunks of channels, one y copy).
 bool staged_path(const UvwSpec& s, const UvwPath& q) {
-  return vector_loads() && q.mul2 == 1 && q.mul1 % kStageU == 0 && q.x_off % 4 == 0 && s.in1 % 4 == 0 &&
+  return s.vec && q.mul2 == 1 && q.mul1 % kStageU == 0 && q.x_off % 4 == 0 && s.in1 % 4 == 0 &&
          (kStageU * q.d1) % 4 == 0;
 }
 
@@ -220,8 +222,7 @@ bool staged_path(const UvwSpec& s, const UvwPath& q) {
 // shared by twice the matrix work; weights staged per chunk through LDS).
 // Needs every path staged and at most 5 output components (160 accumulators).
 bool wide_unit(const UvwSpec& s, const Unit& u) {
-  const char* e = std::getenv("LUNAEQ_AMD_UVW_WIDE");
-  if (e && std::atoi(e) == 0) return false;
+  if (s.wide == 0) return false;
   const UvwPath& head = s.paths[u.paths[0]];
   if (head.d3 > 5 || head.mul3 <= 32) return false;
   for (int p : u.paths)
@@ -234,8 +235,7 @@ bool wide_unit(const UvwSpec& s, const Unit& u) {
 // weights need 16-byte aligned rows, and mul1 whole chunks of kDmaU channels.
 constexpr int kDmaU = 8;
 bool dma_unit(const UvwSpec& s, const Unit& u) {
-  const char* e = std::getenv("LUNAEQ_AMD_UVW_WIDE");
-  if (e && std::atoi(e) != 2) return false;
+  if (s.wide != 2) return false;
   if (!wide_unit(s, u)) return false;
   for (int p : u.paths) {
     const UvwPath& q = s.paths[p];
@@ -252,7 +252,7 @@ int fwd_tiles(const UvwSpec& s, const Unit& u) {
 // Backward paths whose seed rows and weights are staged through LDS in
 // chunks of 16 output channels.
 bool staged_seeds(const UvwSpec& s, const UvwPath& q) {
-  return vector_loads() && q.mul3 % 16 == 0 && q.out_off % 4 == 0 && s.out % 4 == 0 && q.w_off % 4 == 0;
+  return s.vec && q.mul3 % 16 == 0 && q.out_off % 4 == 0 && s.out % 4 == 0 && q.w_off % 4 == 0;
 }
 
 // Sorted distinct (i) and (j) indices of a path's terms.
@@ -775,7 +775,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       std::set<int> unit_is;
       for (int p : un.paths)
         for (int i : term_is(s.paths[p])) unit_is.insert(i);
-      if (vector_loads() && m2 == 1 && Ktot % 16 == 0 && head.x_off % 4 == 0 && s.in1 % 4 == 0) {
+      if (s.vec && m2 == 1 && Ktot % 16 == 0 && head.x_off % 4 == 0 && s.in1 % 4 == 0) {
         // The four K indices of the lane are four consecutive u: 4*d1 floats.
         c.line("    const float4* xv = (const float4*)(xr + (i64)kb * %d);", d1);
         for (int v4 = 0; v4 < d1; ++v4) c.line("    const float4 xq%d = xv[%d];", v4, v4);
@@ -960,7 +960,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 // one path and writes one partial of dW_p; a second kernel sums the partials.
 // Weight-gradient paths whose x, seed and y rows are copied by global_load_lds
 // into two LDS buffers per wave, kWRows rows at a time, the next rows in flight
-// during the current rows' matrix work (LUNAEQ_AMD_UVW_WDMA=0 turns this off).
+// during the current rows' matrix work (UvwSpec::wdma).
 // Rows stay row-major in LDS: a lane reads x[row][u d1 + i] and
 // g[row][w d3 + k] for consecutive u or w, an odd stride, so no bank conflicts.
 constexpr int kWRows = 4;
@@ -970,8 +970,7 @@ int bw_lds_bytes(const UvwPath& q) {
   return 4 * 2 * (bw_pieces(q.mul1 * q.d1) * 4 + bw_pieces(q.mul3 * q.d3) * 4 + 64) * 4;
 }
 bool bw_dma_path(const UvwSpec& s, const UvwPath& q) {
-  const char* e = std::getenv("LUNAEQ_AMD_UVW_WDMA");
-  if (e && std::atoi(e) == 0) return false;
+  if (!s.wdma) return false;
   return q.mul2 == 1 && (q.mul1 * q.d1) % 4 == 0 && (q.mul3 * q.d3) % 4 == 0 && q.x_off % 4 == 0 &&
          q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0 && q.d2 * kWRows <= 64 &&
          bw_lds_bytes(q) <= 128 * 1024;
@@ -1283,6 +1282,12 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     auto holder = std::make_unique<LunaUvwPlan>();
     UvwPlan& p = holder->plan;
     p.spec = parse(spec);
+    const char* vec = std::getenv("LUNAEQ_AMD_UVW_VEC");
+    const char* wide = std::getenv("LUNAEQ_AMD_UVW_WIDE");
+    const char* wdma = std::getenv("LUNAEQ_AMD_UVW_WDMA");
+    p.spec.vec = !vec || std::atoi(vec) != 0;
+    p.spec.wide = wide ? std::atoi(wide) : 2;
+    p.spec.wdma = !wdma || std::atoi(wdma) != 0;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
     p.kernels.tag = "uvw";
