@@ -48,6 +48,7 @@ struct UvwSpec {
   bool vec = true;
   int wide = 2;
   bool wdma = true;
+  int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
 };
 
 constexpr int kChunkRows = 256;  // default batch rows per wave (and per partial) of the weight gradient
@@ -730,16 +731,19 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B) {");
     c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
-    int stage_d3 = 0;
+    int stage_d3 = 0, cw = s.bcw;  // w per staged chunk
     for (const Unit& u : units)
       if (u.phase == phase)
         for (int p : u.paths)
-          if (staged_seeds(s, s.paths[p])) stage_d3 = std::max(stage_d3, s.paths[p].d3);
+          if (staged_seeds(s, s.paths[p])) {
+            stage_d3 = std::max(stage_d3, s.paths[p].d3);
+            if (s.paths[p].mul3 % cw) cw = 16;
+          }
     // The four waves of a workgroup take four K tiles of one input block for
     // the same 16 batch rows and share the staged seed rows.
     if (stage_d3) {
-      c.line("  __shared__ real gs[2][16][%d];", 16 * stage_d3 + 1);
-      c.line("  __shared__ real wsh[4][16][17];");
+      c.line("  __shared__ real gs[2][16][%d];", cw * stage_d3 + 1);
+      c.line("  __shared__ real wsh[4][16][%d];", cw + 1);
       c.line("  int chunk = 0;");
     }
     c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
@@ -810,11 +814,11 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
           for (int j : js) c.line("      real gp%d_%d = 0;", v, j);
         for (int k = 0; k < d3; ++k) c.line("      floatx4 dz%d = (floatx4)(0.0f);", k);
         if (vec) {
-          // Chunks of 16 w: the seed rows of the 16 batch rows and the W rows
+          // Chunks of cw w: the seed rows of the 16 batch rows and the W rows
           // of the 16 K indices go through LDS, read from HBM / L2 with
           // consecutive lanes on consecutive addresses; within a chunk lane
           // group grp takes w = 4 ss + grp.
-          const int gw = 16 * d3;  // floats of one batch row per chunk
+          const int gw = cw * d3;  // floats of one batch row per chunk
           const int total = 16 * gw / 4, per = (total + 255) / 256;
           // Chunk `cc` of the seeds (float4 pieces idx = threadIdx.x + 256 it)
           // and of this wave's W rows into registers.
@@ -825,17 +829,20 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
               c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
               c.line("          const int rr = b0 + r < B ? b0 + r : B - 1;");
               c.line("          if (idx < %d) pg%d = *(const float4*)(g + %d + (%s) * %d + (i64)rr * %d + e * 4);", total, it,
-                     q.out_off, cc, 16 * d3, s.out);
+                     q.out_off, cc, cw * d3, s.out);
               c.line("        }");
             }
-            c.line("        {");
-            c.line("          const int r = lane >> 2, e = lane & 3, kr = kt * 16 + r;");
-            c.line("          pw = kr < %d ? *(const float4*)(wt + %d + (i64)kr * %d + (%s) * 16 + e * 4)"
-                   " : make_float4(0.0f, 0.0f, 0.0f, 0.0f);", Ktot, q.w_off, mul3, cc);
-            c.line("        }");
+            for (int t = 0; t < cw / 16; ++t) {
+              c.line("        {");
+              c.line("          const int pq = lane + %d, r = pq / %d, e = pq - r * %d, kr = kt * 16 + r;", 64 * t, cw / 4,
+                     cw / 4);
+              c.line("          pw%d = kr < %d ? *(const float4*)(wt + %d + (i64)kr * %d + (%s) * %d + e * 4)"
+                     " : make_float4(0.0f, 0.0f, 0.0f, 0.0f);", t, Ktot, q.w_off, mul3, cc, cw);
+              c.line("        }");
+            }
           };
           auto store = [&]() {
-            c.line("        real (*gsb)[%d] = gs[chunk & 1];", 16 * stage_d3 + 1);
+            c.line("        real (*gsb)[%d] = gs[chunk & 1];", cw * stage_d3 + 1);
             for (int it = 0; it < per; ++it) {
               c.line("        {");
               c.line("          const int idx = threadIdx.x + %d;", 256 * it);
@@ -846,25 +853,27 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
               c.line("          }");
               c.line("        }");
             }
-            c.line("        {");
-            c.line("          const int r = lane >> 2, e = lane & 3;");
-            c.line("          real* dst = &wsh[wave][r][e * 4];");
-            c.line("          dst[0] = pw.x; dst[1] = pw.y; dst[2] = pw.z; dst[3] = pw.w;");
-            c.line("        }");
+            for (int t = 0; t < cw / 16; ++t) {
+              c.line("        {");
+              c.line("          const int pq = lane + %d, r = pq / %d, e = pq - r * %d;", 64 * t, cw / 4, cw / 4);
+              c.line("          real* dst = &wsh[wave][r][e * 4];");
+              c.line("          dst[0] = pw%d.x; dst[1] = pw%d.y; dst[2] = pw%d.z; dst[3] = pw%d.w;", t, t, t, t);
+              c.line("        }");
+            }
           };
           for (int it = 0; it < per; ++it) c.line("      float4 pg%d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);", it);
-          c.line("      float4 pw;");
+          for (int t = 0; t < cw / 16; ++t) c.line("      float4 pw%d;", t);
           // Requesting the next chunk before this chunk's matrix work (fenced
           // with sched_barrier) measured the same and spilled registers.
           c.line("      #pragma unroll 1");
-          c.line("      for (int cn = 0; cn < %d; ++cn) {", mul3 / 16);
+          c.line("      for (int cn = 0; cn < %d; ++cn) {", mul3 / cw);
           load("cn");
           store();
           c.line("        __syncthreads();");
           c.line("        const real* gl = &gs[chunk & 1][c16][0];");
           c.line("        const real* al = &wsh[wave][c16][0];");
           c.line("        ++chunk;");
-          for (int ss = 0; ss < 4; ++ss) {
+          for (int ss = 0; ss < cw / 4; ++ss) {
             c.line("        {");
             c.line("          const int wl = %d + grp;", 4 * ss);
             c.line("          const real a = al[wl];");
@@ -1288,6 +1297,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.spec.vec = !vec || std::atoi(vec) != 0;
     p.spec.wide = wide ? std::atoi(wide) : 2;
     p.spec.wdma = !wdma || std::atoi(wdma) != 0;
+    if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
     p.kernels.tag = "uvw";
