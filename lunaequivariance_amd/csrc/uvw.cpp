@@ -49,6 +49,7 @@ struct UvwSpec {
   int wide = 2;
   bool wdma = true;
   int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
+  int wrows = 2;  // LUNAEQ_AMD_UVW_WROWS: batch rows per LDS copy of the weight gradient (2, or 4)
 };
 
 constexpr int kChunkRows = 256;  // default batch rows per wave (and per partial) of the weight gradient
@@ -968,21 +969,20 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
 // instruction and one instruction per k.  Each wave owns kChunkRows rows of
 // one path and writes one partial of dW_p; a second kernel sums the partials.
 // Weight-gradient paths whose x, seed and y rows are copied by global_load_lds
-// into two LDS buffers per wave, kWRows rows at a time, the next rows in flight
+// into two LDS buffers per wave, UvwSpec::wrows rows at a time, the next rows in flight
 // during the current rows' matrix work (UvwSpec::wdma).
 // Rows stay row-major in LDS: a lane reads x[row][u d1 + i] and
 // g[row][w d3 + k] for consecutive u or w, an odd stride, so no bank conflicts.
-constexpr int kWRows = 4;
-int bw_pieces(int floats_per_row) { return (kWRows * floats_per_row / 4 + 63) / 64 * 64; }
+int bw_pieces(const UvwSpec& s, int floats_per_row) { return (s.wrows * floats_per_row / 4 + 63) / 64 * 64; }
 // LDS of a workgroup (four waves, two buffers of x, seed and y rows) for one path.
-int bw_lds_bytes(const UvwPath& q) {
-  return 4 * 2 * (bw_pieces(q.mul1 * q.d1) * 4 + bw_pieces(q.mul3 * q.d3) * 4 + 64) * 4;
+int bw_lds_bytes(const UvwSpec& s, const UvwPath& q) {
+  return 4 * 2 * (bw_pieces(s, q.mul1 * q.d1) * 4 + bw_pieces(s, q.mul3 * q.d3) * 4 + 64) * 4;
 }
 bool bw_dma_path(const UvwSpec& s, const UvwPath& q) {
   if (!s.wdma) return false;
   return q.mul2 == 1 && (q.mul1 * q.d1) % 4 == 0 && (q.mul3 * q.d3) % 4 == 0 && q.x_off % 4 == 0 &&
-         q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0 && q.d2 * kWRows <= 64 &&
-         bw_lds_bytes(q) <= 128 * 1024;
+         q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0 && q.d2 * s.wrows <= 64 &&
+         bw_lds_bytes(s, q) <= 128 * 1024;
 }
 
 // All such paths in one function (four __restrict__ buffers, so the
@@ -998,9 +998,9 @@ void emit_bw_dma(Code& c, const UvwSpec& s, int chunk_rows) {
     if (!bw_dma_path(s, q)) continue;
     const int K = q.mul1, mt = ktiles(q), nt = (q.mul3 + 31) / 32, d3 = q.d3, d1 = q.d1;
     const int px = q.mul1 * d1, pg = q.mul3 * d3;  // floats per row of the x block and of the seed block
-    const int nx = bw_pieces(px) / 64, ng = bw_pieces(pg) / 64, ncopy = nx + ng + 1;
+    const int nx = bw_pieces(s, px) / 64, ng = bw_pieces(s, pg) / 64, ncopy = nx + ng + 1;
     const int d2 = q.d2;
-    const int nch = chunk_rows / kWRows;
+    const int nch = chunk_rows / s.wrows;
     const std::set<int> is = term_is(q), js = term_js(q);
     c.line("  if (path == %d) {", p);
     for (int m = 0; m < mt; ++m)
@@ -1016,19 +1016,19 @@ void emit_bw_dma(Code& c, const UvwSpec& s, int chunk_rows) {
     // Copy instruction i, lane l: 16-byte piece 64 i + l of the rows, row-major
     // (pieces past the rows re-read the last piece into the buffer's tail).
     for (int i = 0; i < nx; ++i) {
-      c.line("    const int xpc%d = 64 * %d + lane < %d ? 64 * %d + lane : %d;", i, i, kWRows * px / 4, i,
-             kWRows * px / 4 - 1);
+      c.line("    const int xpc%d = 64 * %d + lane < %d ? 64 * %d + lane : %d;", i, i, s.wrows * px / 4, i,
+             s.wrows * px / 4 - 1);
       c.line("    const int xrow%d = xpc%d / %d, xoff%d = %d + (xpc%d - xrow%d * %d) * 4;", i, i, px / 4, i, q.x_off, i, i,
              px / 4);
     }
     for (int i = 0; i < ng; ++i) {
-      c.line("    const int gpc%d = 64 * %d + lane < %d ? 64 * %d + lane : %d;", i, i, kWRows * pg / 4, i,
-             kWRows * pg / 4 - 1);
+      c.line("    const int gpc%d = 64 * %d + lane < %d ? 64 * %d + lane : %d;", i, i, s.wrows * pg / 4, i,
+             s.wrows * pg / 4 - 1);
       c.line("    const int grow%d = gpc%d / %d, goff%d = %d + (gpc%d - grow%d * %d) * 4;", i, i, pg / 4, i, q.out_off, i,
              i, pg / 4);
     }
     // y: one 4-byte copy per lane, lane l = (row l / d2, column l % d2).
-    c.line("    const int yl = lane < %d ? lane : %d;", kWRows * d2, kWRows * d2 - 1);
+    c.line("    const int yl = lane < %d ? lane : %d;", s.wrows * d2, s.wrows * d2 - 1);
     c.line("    const int yrow = yl / %d, ycol = %d + yl - yrow * %d;", d2, q.y_off, d2);
     auto copy = [&](const char* cb, const char* X, const char* G, const char* Y) {
       for (int i = 0; i < nx; ++i)
@@ -1045,7 +1045,7 @@ void emit_bw_dma(Code& c, const UvwSpec& s, int chunk_rows) {
       c.line("      __builtin_amdgcn_sched_barrier(0);");
     };
     auto compute = [&](const char* cb, const char* X, const char* G, const char* Y) {
-      for (int sp = 0; sp < kWRows / 2; ++sp) {
+      for (int sp = 0; sp < s.wrows / 2; ++sp) {
         c.line("      {");
         c.line("        const bool rok = %s + %d + hk < B;", cb, 2 * sp);
         for (int j : js) c.line("        const real y%d_%d = %s[(%d + hk) * %d + %d];", sp, j, Y, 2 * sp, d2, j);
@@ -1073,12 +1073,12 @@ void emit_bw_dma(Code& c, const UvwSpec& s, int chunk_rows) {
     c.line("    }");
     c.line("    #pragma unroll 1");
     c.line("    for (int cc = 0; cc < %d; cc += 2) {", nch);
-    c.line("      const int ca = r0 + cc * %d, cb = ca + %d;", kWRows, kWRows);
+    c.line("      const int ca = r0 + cc * %d, cb = ca + %d;", s.wrows, s.wrows);
     copy("cb", "X1", "G1", "Y1");
     wait(ncopy);
     compute("ca", "X0", "G0", "Y0");
     c.line("      if (cc + 2 < %d) {", nch);
-    const std::string next = "cb + " + std::to_string(kWRows);
+    const std::string next = "cb + " + std::to_string(s.wrows);
     copy(next.c_str(), "X0", "G0", "Y0");
     wait(ncopy);
     c.line("      } else {");
@@ -1111,8 +1111,8 @@ std::string emit_backward_w(const UvwSpec& s, int chunk_rows) {
   int xmax = 0, gmax = 0;
   for (const auto& q : s.paths)
     if (bw_dma_path(s, q)) {
-      xmax = std::max(xmax, bw_pieces(q.mul1 * q.d1) * 4);
-      gmax = std::max(gmax, bw_pieces(q.mul3 * q.d3) * 4);
+      xmax = std::max(xmax, bw_pieces(s, q.mul1 * q.d1) * 4);
+      gmax = std::max(gmax, bw_pieces(s, q.mul3 * q.d3) * 4);
     }
   if (xmax) emit_bw_dma(c, s, chunk_rows);
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvw_bwd_w(");
@@ -1297,6 +1297,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.spec.vec = !vec || std::atoi(vec) != 0;
     p.spec.wide = wide ? std::atoi(wide) : 2;
     p.spec.wdma = !wdma || std::atoi(wdma) != 0;
+    if (const char* wr = std::getenv("LUNAEQ_AMD_UVW_WROWS")) p.spec.wrows = std::atoi(wr) == 4 ? 4 : 2;
     if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
