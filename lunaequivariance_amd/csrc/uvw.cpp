@@ -48,6 +48,7 @@ struct UvwSpec {
   bool vec = true;
   int wide = 2;
   bool wdma = true;
+  int gpad = 4;  // LUNAEQ_AMD_UVW_GPAD: seed-row padding in the gx/gy staging (1: scalar LDS writes)
   int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
   int wrows = 2;  // LUNAEQ_AMD_UVW_WROWS: batch rows per LDS copy of the weight gradient (2, or 4)
 };
@@ -743,7 +744,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
     // The four waves of a workgroup take four K tiles of one input block for
     // the same 16 batch rows and share the staged seed rows.
     if (stage_d3) {
-      c.line("  __shared__ real gs[2][16][%d];", cw * stage_d3 + 1);
+      c.line("  __shared__ __attribute__((aligned(16))) real gs[2][16][%d];", cw * stage_d3 + s.gpad);
       c.line("  __shared__ real wsh[4][16][%d];", cw + 1);
       c.line("  int chunk = 0;");
     }
@@ -843,14 +844,17 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
             }
           };
           auto store = [&]() {
-            c.line("        real (*gsb)[%d] = gs[chunk & 1];", cw * stage_d3 + 1);
+            c.line("        real (*gsb)[%d] = gs[chunk & 1];", cw * stage_d3 + s.gpad);
             for (int it = 0; it < per; ++it) {
               c.line("        {");
               c.line("          const int idx = threadIdx.x + %d;", 256 * it);
               c.line("          const int r = idx / %d, e = idx - r * %d;", gw / 4, gw / 4);
               c.line("          if (idx < %d) {", total);
               c.line("            real* dst = &gsb[r][e * 4];");
-              c.line("            dst[0] = pg%d.x; dst[1] = pg%d.y; dst[2] = pg%d.z; dst[3] = pg%d.w;", it, it, it, it);
+              if (s.gpad == 4)
+                c.line("            *(float4*)dst = pg%d;", it);
+              else
+                c.line("            dst[0] = pg%d.x; dst[1] = pg%d.y; dst[2] = pg%d.z; dst[3] = pg%d.w;", it, it, it, it);
               c.line("          }");
               c.line("        }");
             }
@@ -1298,6 +1302,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.spec.wide = wide ? std::atoi(wide) : 2;
     p.spec.wdma = !wdma || std::atoi(wdma) != 0;
     if (const char* wr = std::getenv("LUNAEQ_AMD_UVW_WROWS")) p.spec.wrows = std::atoi(wr) == 4 ? 4 : 2;
+    if (const char* gp = std::getenv("LUNAEQ_AMD_UVW_GPAD")) p.spec.gpad = std::atoi(gp) == 1 ? 1 : 4;
     if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
