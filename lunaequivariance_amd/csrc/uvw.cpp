@@ -237,18 +237,25 @@ bool wide_unit(const UvwSpec& s, const Unit& u) {
 // double-buffered: the next chunk streams in while the current one is used):
 // weights need 16-byte aligned rows, and mul1 whole chunks of kDmaU channels.
 constexpr int kDmaU = 8;
-bool dma_unit(const UvwSpec& s, const Unit& u) {
-  if (s.wide != 2) return false;
-  if (!wide_unit(s, u)) return false;
+// Units that do not qualify as wide (more than 5 output components, or at
+// most 32 channels) take the same LDS copies with one 32-channel tile per
+// wave, up to 9 components (144 accumulators).
+int dma_tiles(const UvwSpec& s, const Unit& u) {
+  if (s.wide != 2) return 0;
+  const UvwPath& head = s.paths[u.paths[0]];
   for (int p : u.paths) {
     const UvwPath& q = s.paths[p];
-    if (q.mul3 % 4 || q.w_off % 4 || q.mul1 % kDmaU || q.d1 > 7) return false;
+    if (!staged_path(s, q) || q.mul3 % 4 || q.w_off % 4 || q.mul1 % kDmaU || q.d1 > 7) return 0;
   }
-  return true;
+  if (wide_unit(s, u)) return 2;
+  return head.d3 <= 9 ? 1 : 0;
 }
+bool dma_unit(const UvwSpec& s, const Unit& u) { return dma_tiles(s, u) > 0; }
 
 int fwd_tiles(const UvwSpec& s, const Unit& u) {
   const int mul3 = s.paths[u.paths[0]].mul3;
+  const int dt = dma_tiles(s, u);
+  if (dt) return (mul3 + 32 * dt - 1) / (32 * dt);
   return wide_unit(s, u) ? (mul3 + 63) / 64 : (mul3 + 31) / 32;
 }
 
@@ -411,7 +418,7 @@ void emit_forward_wide(Code& c, const UvwSpec& s, const Unit& u, int nt) {
 // that buffer (without the scopes it waits for every copy in flight).
 void emit_dma_unit_body(Code& c, const UvwSpec& s, const Unit& u) {
   const UvwPath& head = s.paths[u.paths[0]];
-  const int d3 = head.d3, mul3 = head.mul3;
+  const int d3 = head.d3, mul3 = head.mul3, T = dma_tiles(s, u), wq = 8 * T;  // wq: 16-byte pieces per K row
   for (int p : u.paths) {
     const UvwPath& q = s.paths[p];
     const std::set<int> is = term_is(q), js = term_js(q);
@@ -420,19 +427,23 @@ void emit_dma_unit_body(Code& c, const UvwSpec& s, const Unit& u) {
     c.line("    const real* ys = y + (i64)brow * %d + %d;", s.in2, q.y_off);
     for (int j : js) c.line("    const real y%d = ys[%d];", j, j);
     c.line("    const real* xrow = x + (i64)rrow * %d + %d + (lane >> 5) * 4;", s.in1, q.x_off);
-    c.line("    const real* wrow = wt + %d + (i64)(lane >> 4) * %d + wl;", q.w_off, mul3);
+    c.line("    const real* wrow = wt + %d + (i64)(lane / %d) * %d + wl;", q.w_off, wq, mul3);
     auto copy = [&](const char* chunk, const char* X, const char* W) {
       for (int i = 0; i < d1; ++i)
         c.line("      __builtin_amdgcn_global_load_lds((const void*)(xrow + (%s) * %d + %d), (lvoid*)(%s + %d), 16, 0, 0);",
                chunk, kDmaU * d1, 8 * i, X, 256 * i);
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < T; ++i)
         c.line("      __builtin_amdgcn_global_load_lds((const void*)(wrow + (i64)((%s) * %d + %d) * %d), "
                "(lvoid*)(%s + %d), 16, 0, 0);",
-               chunk, kDmaU, 4 * i, mul3, W, 256 * i);
+               chunk, kDmaU, 64 / wq * i, mul3, W, 256 * i);
     };
     // Wait until only `left` copies are in flight (vmcnt counts in issue order).
+    // The empty asm with a memory clobber keeps the optimizer from moving LDS
+    // reads above the wait (the wait intrinsic itself does not order memory
+    // accesses); sched_barrier does the same for the machine scheduler.
     auto wait = [&](int left) {
       c.line("      __builtin_amdgcn_s_waitcnt(%d);", vmcnt_imm(left));
+      c.line("      asm volatile(\"\" ::: \"memory\");");
       c.line("      __builtin_amdgcn_sched_barrier(0);");
     };
     auto compute = [&](const char* X, const char* W) {
@@ -445,20 +456,18 @@ void emit_dma_unit_body(Code& c, const UvwSpec& s, const Unit& u) {
         for (int pc : pieces) c.line("          const float4 q%d = xp[%d];", pc, 32 * pc);
         for (int i : is)
           c.line("          const real x%d = q%d.%c;", i, (st * d1 + i) / 4, "xyzw"[(st * d1 + i) % 4]);
-        c.line("          const real a0 = %s[(%d + 4 * hk) * 64 + col], a1 = %s[(%d + 4 * hk) * 64 + 32 + col];", W, st,
-               W, st);
+        for (int t = 0; t < T; ++t)
+          c.line("          const real a%d = %s[(%d + 4 * hk) * %d + %d + col];", t, W, st, 32 * T, 32 * t);
         for (int k = 0; k < d3; ++k) c.line("          real z%d = 0;", k);
         for (const auto& t : q.terms)
           c.line("          z%d = FMA(%s, x%d * y%d, z%d);", t.k, flit(t.c).c_str(), t.i, t.j, t.k);
-        for (int k = 0; k < d3; ++k) {
-          c.line("          acc[0][%d] = mfma32(a0, z%d, acc[0][%d]);", k, k, k);
-          c.line("          acc[1][%d] = mfma32(a1, z%d, acc[1][%d]);", k, k, k);
-        }
+        for (int k = 0; k < d3; ++k)
+          for (int t = 0; t < T; ++t) c.line("          acc[%d][%d] = mfma32(a%d, z%d, acc[%d][%d]);", t, k, t, k, t, k);
         c.line("        }");
       }
       c.line("      }");
     };
-    const int ncopy = d1 + 2;
+    const int ncopy = d1 + T;
     c.line("    {");
     copy("0", "X0", "W0");
     c.line("    }");
@@ -483,19 +492,19 @@ void emit_dma_unit_body(Code& c, const UvwSpec& s, const Unit& u) {
 // after storing; others move `unit` past it.
 void emit_forward_dma(Code& c, const UvwSpec& s, const Unit& u, int nt) {
   const UvwPath& head = s.paths[u.paths[0]];
-  const int d3 = head.d3, mul3 = head.mul3;
+  const int d3 = head.d3, mul3 = head.mul3, T = dma_tiles(s, u), wq = 8 * T;
   c.line("  if (unit < %d) {", nt);
-  c.line("    const int w0 = unit * 64;");
-  c.line("    floatx16 acc[2][%d];", d3);
-  for (int t = 0; t < 2; ++t)
+  c.line("    const int w0 = unit * %d;", 32 * T);
+  c.line("    floatx16 acc[%d][%d];", T, d3);
+  for (int t = 0; t < T; ++t)
     for (int k = 0; k < d3; ++k) c.line("    acc[%d][%d] = (floatx16)(0.0f);", t, k);
-  c.line("    const int wl = (w0 + (lane & 15) * 4 < %d) ? w0 + (lane & 15) * 4 : %d;", mul3, mul3 - 4);
+  c.line("    const int wl = (w0 + (lane %% %d) * 4 < %d) ? w0 + (lane %% %d) * 4 : %d;", wq, mul3, wq, mul3 - 4);
   emit_dma_unit_body(c, s, u);
   c.line("    if (b0 + col < B) {");
   c.line("      real* orow = out + (i64)(b0 + col) * %d + %d;", s.out, head.out_off);
   c.line("      #pragma unroll");
   c.line("      for (int r = 0; r < 16; ++r) {");
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < T; ++t) {
     c.line("        {");
     c.line("          const int w = w0 + %d + 8 * (r >> 2) + 4 * hk + (r & 3);", 32 * t);
     c.line("          if (w < %d) {", mul3);
@@ -521,8 +530,13 @@ void emit_forward_dma_phase(Code& c, const UvwSpec& s, const std::vector<Unit>& 
   c.line("  const int rrow = b0 + col < B ? b0 + col : B - 1;");
   for (const Unit& u : units) {
     if (u.phase != phase) continue;
-    if (dma_unit(s, u)) emit_forward_dma(c, s, u, fwd_tiles(s, u));
-    else c.line("  unit -= %d;", fwd_tiles(s, u));
+    if (dma_unit(s, u)) {
+      emit_forward_dma(c, s, u, fwd_tiles(s, u));
+    } else {
+      // A tile of another kind of unit: the kernel body computes it.
+      c.line("  if (unit < %d) return false;", fwd_tiles(s, u));
+      c.line("  unit -= %d;", fwd_tiles(s, u));
+    }
   }
   c.line("  return false;");
   c.line("}");
@@ -1044,8 +1058,12 @@ void emit_bw_dma(Code& c, const UvwSpec& s, int chunk_rows) {
       c.line("      __builtin_amdgcn_global_load_lds((const void*)(y + (i64)min(%s + yrow, B - 1) * %d + ycol), "
              "(lvoid*)%s, 4, 0, 0);", cb, s.in2, Y);
     };
+    // The empty asm with a memory clobber keeps the optimizer from moving LDS
+    // reads above the wait (the wait intrinsic itself does not order memory
+    // accesses); sched_barrier does the same for the machine scheduler.
     auto wait = [&](int left) {
       c.line("      __builtin_amdgcn_s_waitcnt(%d);", vmcnt_imm(left));
+      c.line("      asm volatile(\"\" ::: \"memory\");");
       c.line("      __builtin_amdgcn_sched_barrier(0);");
     };
     auto compute = [&](const char* cb, const char* X, const char* G, const char* Y) {

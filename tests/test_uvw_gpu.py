@@ -22,6 +22,7 @@ DEV = "cuda"
     ("96x0e+16x1o", "1x0e+2x1o", "48x0e+40x1o+8x2e", 70),                   # K > 64, mul2 = 2, odd mul3
     ("32x0e+32x1o", "1x0e+1x1o", "48x0e+50x1o+8x2e", 70),                   # LDS-copied, 64-wide and narrow units
     ("64x0e+32x1o", "2x0e+1x1o", "64x0e+64x1o", 50),                        # mul2 = 2 with 32-w seed chunks
+    ("16x0e+16x1o", "1x0e+1x1o", "64x0e+64x1o+16x2e", 45),                  # two LDS-copied chunks per path
 ])
 def test_uvw_forward_and_two_orders(in1, in2, out, rows):
     instructions = uvw_instructions(in1, in2, out)
