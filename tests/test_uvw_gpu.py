@@ -162,3 +162,44 @@ def test_uvw_wide_blocks():
     dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32))
     for n, (a, r) in enumerate(zip(dev_first, ref_first)):
         assert_close(a, r, torch.float32, f"first-order {n}")
+
+
+def _random_layouts(count, seed):
+    import random
+
+    rnd = random.Random(seed)
+    muls = [8, 16, 24, 32, 48, 64, 96, 128]
+
+    def irreps(lmax, pick):
+        return "+".join(f"{pick()}x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(lmax + 1))
+
+    out = []
+    while len(out) < count:
+        a = irreps(rnd.randint(1, 3), lambda: rnd.choice(muls))
+        b = irreps(rnd.randint(1, 3), lambda: rnd.choice([1, 1, 2]))
+        c = irreps(rnd.randint(1, 3), lambda: rnd.choice(muls))
+        if uvw_instructions(a, b, c):
+            out.append((a, b, c, rnd.choice([1, 17, 70, 257])))
+    return out
+
+
+@pytest.mark.parametrize("in1,in2,out,rows", _random_layouts(6, 1))
+def test_uvw_random_layouts(in1, in2, out, rows):
+    """Seeded random layouts (multiplicities 8-128, degrees up to 3, one or two
+    edge copies): every kernel variant and launch split against the oracle."""
+    instructions = uvw_instructions(in1, in2, out)
+    tp = lunaeq.TensorProduct(in1, in2, out, instructions, shared_weights=True, internal_weights=False)
+    gen = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64) / 8
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ref = uvw_tensor_product(in1, in2, out, instructions, *ref_in)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in)
+    assert_close(act, ref, torch.float32, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    ref_first = torch.autograd.grad(ref, ref_in, g)
+    dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32))
+    for n, (a, r) in enumerate(zip(dev_first, ref_first)):
+        assert_close(a, r, torch.float32, f"first-order {n}")
