@@ -48,6 +48,7 @@ struct UvwSpec {
   bool vec = true;
   int wide = 2;
   bool wdma = true;
+  int bcy = -1;  // LUNAEQ_AMD_UVW_BCY: gx/gy contraction as (c y) dZ (1) or c (y dZ) (0); -1: by occupancy
   int gpad = 4;  // LUNAEQ_AMD_UVW_GPAD: seed-row padding in the gx/gy staging (1: scalar LDS writes)
   int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
   int wrows = 2;  // LUNAEQ_AMD_UVW_WROWS: batch rows per LDS copy of the weight gradient (2, or 4)
@@ -744,6 +745,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
     }
     c.line("extern \"C\" __global__ void __launch_bounds__(256) %sluna_uvw_bwd_xy_p%d(",
            four ? "__attribute__((amdgpu_waves_per_eu(4))) " : "__attribute__((amdgpu_waves_per_eu(2))) ", phase);
+    const bool cy_form = s.bcy < 0 ? four : s.bcy != 0;
     c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
     c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B) {");
     c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
@@ -913,12 +915,20 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
         for (int r = 0; r < 4; ++r) {
           const int v = r % m2, qd = r / m2;
           for (const auto& t : q.terms) {
-            // c * (y dZ), not (c y) * dZ: products of a coefficient and an
-            // operand would be shared across the four K rows and kept live.
-            c.line("      gxa%d_%d = FMA(%s, y%d_%d * dz%d[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, t.k, r,
-                   qd, t.i);
-            c.line("      gp%d_%d = FMA(%s, x%d_%d * dz%d[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, t.k, r, v,
-                   t.j);
+            // (c y) dZ shares the products c y across the four K rows (one
+            // VALU op per term and row); c (y dZ) keeps no products live (two
+            // ops), for kernels short of registers.
+            if (cy_form) {
+              c.line("      gxa%d_%d = FMA(%s * y%d_%d, dz%d[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, t.k,
+                     r, qd, t.i);
+              c.line("      gp%d_%d = FMA(%s * x%d_%d, dz%d[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, t.k, r,
+                     v, t.j);
+            } else {
+              c.line("      gxa%d_%d = FMA(%s, y%d_%d * dz%d[%d], gxa%d_%d);", qd, t.i, flit(t.c).c_str(), v, t.j, t.k,
+                     r, qd, t.i);
+              c.line("      gp%d_%d = FMA(%s, x%d_%d * dz%d[%d], gp%d_%d);", v, t.j, flit(t.c).c_str(), r, t.i, t.k, r,
+                     v, t.j);
+            }
           }
         }
         // Sum over the four lane groups that share a batch row.
@@ -1320,6 +1330,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.spec.wide = wide ? std::atoi(wide) : 2;
     p.spec.wdma = !wdma || std::atoi(wdma) != 0;
     if (const char* wr = std::getenv("LUNAEQ_AMD_UVW_WROWS")) p.spec.wrows = std::atoi(wr) == 4 ? 4 : 2;
+    if (const char* cy = std::getenv("LUNAEQ_AMD_UVW_BCY")) p.spec.bcy = std::atoi(cy);
     if (const char* gp = std::getenv("LUNAEQ_AMD_UVW_GPAD")) p.spec.gpad = std::atoi(gp) == 1 ? 1 : 4;
     if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
 
