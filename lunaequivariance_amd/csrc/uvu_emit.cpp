@@ -27,6 +27,7 @@
 #include <map>
 #include <set>
 #include <sstream>
+#include <tuple>
 
 #include "uvu_plan.h"
 
@@ -516,7 +517,7 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
 // One wave's share of a backward group: all of its paths, or one subset of
 // a split group (`g` is then the subset's view, sub its index).
 void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
-                        bool want_msg, bool want_part, const Options& opt, int sub) {
+                        bool want_msg, bool want_part, const Options& opt, int sub, bool cmajor) {
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
   const int np = (int)g.paths.size();
@@ -673,15 +674,22 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
   if (want_msg && sub == 0) {
     // Lanes past the last channel repeat channel C-1 exactly, so their stores
     // write identical values; only the cross-lane sums below must mask them.
+    // Component-major messages: component i of the 64 channels of a chunk is
+    // one contiguous 256-byte run (full-line stores; the x layout, d1 values
+    // per lane, made every store a strided partial-line write).
+    const int stride = cmajor ? g.channels : 1;
     c.line("      {");
-    c.line("        real* mr = msg + (i64)e * IN1 + (%d + uc * %d);", g.x_off, g.d1);
+    if (cmajor)
+      c.line("        real* mr = msg + (i64)e * IN1 + (%d + uc);", g.x_off);
+    else
+      c.line("        real* mr = msg + (i64)e * IN1 + (%d + uc * %d);", g.x_off, g.d1);
     for (int i = 0; i < g.d1; ++i) {
       if (g.gx_accumulate)
-        c.line("        mr[%d] += M%d;", i, i);
+        c.line("        mr[%d] += M%d;", i * stride, i);
       else if (opt.nt_msg)
-        c.line("        __builtin_nontemporal_store(M%d, mr + %d);", i, i);
+        c.line("        __builtin_nontemporal_store(M%d, mr + %d);", i, i * stride);
       else
-        c.line("        mr[%d] = M%d;", i, i);
+        c.line("        mr[%d] = M%d;", i * stride, i);
     }
     c.line("      }");
   }
@@ -714,15 +722,15 @@ Group subset_view(const Group& g, int sub) {
 }
 
 void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
-                         bool want_msg, bool want_part, const Options& opt) {
+                         bool want_msg, bool want_part, const Options& opt, bool cmajor) {
   if (g.subsets == 1) {
-    emit_backward_wave(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt, 0);
+    emit_backward_wave(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt, 0, cmajor);
     return;
   }
   c.line("    const int sub = (slot - %d) %% %d;", g.slot_base, g.subsets);
   for (int sub = 0; sub < g.subsets; ++sub) {
     c.line("    %sif (sub == %d) {", sub ? "else " : "", sub);
-    emit_backward_wave(c, spec, subset_view(g, sub), env, gl0, want_gw, want_msg, want_part, opt, sub);
+    emit_backward_wave(c, spec, subset_view(g, sub), env, gl0, want_gw, want_msg, want_part, opt, sub, cmajor);
     c.line("    }");
   }
 }
@@ -786,6 +794,7 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   if (opt.bwd_nt_w < 0) opt.bwd_nt_w = streaming;
   if (opt.nt_msg < 0) opt.nt_msg = streaming;
   opt.nt_w = opt.bwd_nt_w != 0;
+  const bool cmajor = message_component_major(plan);
   Code c;
   c.raw(prelude(spec));
   for (int phase = 0; phase < plan.bwd_phases; ++phase) {
@@ -821,7 +830,7 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
       c.line("  %sif (slot >= %d && slot < %d) {", first ? "" : "else ", g.slot_base,
              g.slot_base + g.chunks * g.subsets);
       first = false;
-      emit_backward_group(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt);
+      emit_backward_group(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt, cmajor);
       c.line("  }");
     }
     c.line("}");
@@ -900,6 +909,20 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     else
       merged.push_back(r);
   }
+  // Position in gx of message column col (component-major blocks permute).
+  c.line("__device__ __forceinline__ int gx_col(int col) {");
+  if (cmajor) {
+    std::set<std::tuple<int, int, int>> blocks;
+    for (const Group& g : plan.bwd_groups) blocks.insert({g.x_off, g.d1, g.channels});
+    for (const auto& b : blocks) {
+      const int x0 = std::get<0>(b), d1 = std::get<1>(b), ch = std::get<2>(b);
+      if (d1 == 1) continue;
+      c.line("  if (col >= %d && col < %d) { const int r = col - %d; return %d + (r %% %d) * %d + r / %d; }", x0,
+             x0 + ch * d1, x0, x0, ch, d1, ch);
+    }
+  }
+  c.line("  return col;");
+  c.line("}");
   c.line("__device__ __forceinline__ bool covered(int col) {");
   if (merged.size() == 1 && merged[0].first == 0 && merged[0].second == spec.in1) {
     c.line("  return true;");
@@ -940,7 +963,18 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   // pairwise sum of the partial accumulators
   for (int width = 1; width < un; width *= 2)
     for (int n = 0; n + width < un; n += 2 * width) c.line("  acc%d += acc%d;", n, n + width);
-  c.line("  *(vec_t*)(gx + (i64)s * IN1 + col) = acc0;");
+  if (cmajor && vec > 1) {
+    // The values of one vector are consecutive channels of one component:
+    // their gx positions are d1 apart.
+    c.line("  real* gr = gx + (i64)s * IN1;");
+    c.line("  const int g0 = gx_col(col);");
+    c.line("  const int step = %d > 1 ? gx_col(col + 1) - g0 : 1;", vec);
+    for (int n = 0; n < vec; ++n) c.line("  gr[g0 + %d * step] = acc0[%d];", n, n);
+  } else if (cmajor) {
+    c.line("  gx[(i64)s * IN1 + gx_col(col)] = acc0;");
+  } else {
+    c.line("  *(vec_t*)(gx + (i64)s * IN1 + col) = acc0;");
+  }
   c.line("}");
   return c.s.str();
 }

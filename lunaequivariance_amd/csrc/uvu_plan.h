@@ -81,6 +81,12 @@ Spec parse_spec(const std::string& text);
 // Elements per access of the gx gather: 16-byte vectors when every covered
 // input range and the row length are multiples of it, else 1.
 int gather_vector_width(const Plan& plan);
+// True when the gx messages are stored component-major per input block
+// (msg[e, x_off + i * C + u]: every store of a wave is 64 contiguous values)
+// instead of in the x layout (msg[e, x_off + u * d1 + i]); the gather kernel
+// then permutes back.  Requires the groups' input ranges to be identical or
+// disjoint.  LUNAEQ_AMD_MSGCM=0 selects the x layout.
+bool message_component_major(const Plan& plan);
 void build_schedule(Plan& plan);
 
 // Emitted HIP source of one kernel module variant.

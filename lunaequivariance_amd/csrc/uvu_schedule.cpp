@@ -189,13 +189,32 @@ int assign_phases(std::vector<Group>& groups, RangesOf ranges_of) {
 
 }  // namespace
 
+bool message_component_major(const Plan& plan) {
+  if (const char* e = std::getenv("LUNAEQ_AMD_MSGCM"))
+    if (std::atoi(e) == 0) return false;
+  for (size_t a = 0; a < plan.bwd_groups.size(); ++a) {
+    for (size_t b = a + 1; b < plan.bwd_groups.size(); ++b) {
+      const Group& p = plan.bwd_groups[a];
+      const Group& q = plan.bwd_groups[b];
+      const bool same = p.x_off == q.x_off && p.d1 == q.d1 && p.channels == q.channels;
+      if (!same && ranges_overlap(p.x_off, p.x_off + (long)p.channels * p.d1, q.x_off,
+                                  q.x_off + (long)q.channels * q.d1))
+        return false;
+    }
+  }
+  return true;
+}
+
 int gather_vector_width(const Plan& plan) {
   const Spec& spec = plan.spec;
   int vec = 16 / (spec.dtype_bits / 8);
+  const bool cmajor = message_component_major(plan);
   bool aligned = spec.in1 % vec == 0;
   for (const Group& g : plan.bwd_groups) {
     const long end = g.x_off + (long)g.channels * g.d1;
     aligned = aligned && g.x_off % vec == 0 && end % vec == 0;
+    // Component-major: the values of one vector must share their component.
+    if (cmajor) aligned = aligned && g.channels % vec == 0;
   }
   return aligned ? vec : 1;
 }
