@@ -13,7 +13,7 @@ from .modules import TensorProduct, TensorProductConv
 from .uvu_conv import create_uvu_conv_operator
 from .uuu_conv import create_uuu_conv_operator
 from .cg import wigner_3j
-from . import ops  # registers the lunaeq_amd:: dispatcher operators
+from . import ops  # registers the lunatp:: dispatcher operators
 
 __all__ = [
     "Irrep", "Irreps", "TensorProductConfig", "TensorProductPaths", "Instruction",

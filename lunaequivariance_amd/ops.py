@@ -1,14 +1,37 @@
-"""Dispatcher operators for ``torch.compile`` / export.
+"""Dispatcher operators for ``torch.compile`` / export, under the reference's names.
 
-Mirror of the reference's ``lunatp::uvu_conv_forward`` / ``_backward``
-custom ops (``src/lunatp/uvu_conv/interface.py:18-140``) and
-``lunatp::uuu_conv_forward`` / ``_backward``
-(``src/lunatp/uuu_conv/interface.py:15-150``) under the ``lunaeq_amd``
-namespace: tensors, graph tables and a JSON string of the
-static configuration go in; fake kernels give output shapes; autograd of the
-forward op calls the backward op, and autograd of the backward op composes
-forward and backward ops with cotangent-substituted arguments (the
-convolution is multilinear), so compiled graphs differentiate to any order.
+The reference registers four custom ops per convolution mode with fixed
+schemas (``src/lunatp/uvu_conv/interface.py:18-89``,
+``src/lunatp/uuu_conv/interface.py:15-95``):
+
+  lunatp::{uvu,uuu}_conv_forward          (x, y, w, env?, tables, num_nodes, return_l0, config)
+  lunatp::{uvu,uuu}_conv_backward         (..., g, gl0?, tables, num_nodes, needs[4], config)
+  lunatp::{uvu,uuu}_conv_double_backward  (..., g, gl0?, rx, ry, rw, re?, tables, num_nodes, needs[6], config)
+  lunatp::{uvu,uuu}_conv_triple_backward  (..., rx..re?, sx, sy, sw, sg, se?, sl0?, tables, num_nodes, needs[10], config)
+
+This module registers the same names and schemas, so a graph traced or
+exported against the reference's ops runs here unchanged:
+
+* ``tables`` is the reference's 13-entry list, in its order
+  (``uvu_conv/interface.py:186-192``): src, dst, dst_rowptr, src_rowptr,
+  edge_ids_by_src, source_node_order, node_order, the five source-segment
+  tables (nodes, begin, end, rowptr, order) and node_tiers.  The kernels read
+  the first seven.
+* ``config`` is the reference's static-configuration string
+  (``src/lunatp/interface.py:57-73`` with ``src/utils/operator_config.py``):
+  JSON of {mode, dtype, index_bits, out_dim, l0_dim, weight_mode, meta}, with
+  tuples and dtypes tagged.  Configurations written by either implementation
+  decode to the same prepared operator.
+* Cotangents that are absent inside this module's own autograd are passed as
+  0-element tensors, which the derivative ops treat as zero (skipping their
+  kernels); materialised zeros, as the reference passes them, give the same
+  result.
+
+Every op runs HIP kernels only: the first-order ops launch the forward and
+backward kernels, the double backward composes them with arguments replaced
+by cotangents (the convolution is multilinear in x, y, w, env and linear in
+the output seeds), and the triple backward does the same with two arguments
+replaced (``_triple`` derives the terms).
 """
 
 from __future__ import annotations
@@ -19,7 +42,10 @@ from functools import lru_cache
 
 import torch
 
-GRAPH_TABLES = ("src", "dst", "dst_rowptr", "src_rowptr", "edge_ids_by_src", "node_order", "source_node_order")
+# Reference order of the graph tables (``uvu_conv/interface.py:186-192``).
+GRAPH_TABLES = ("src", "dst", "dst_rowptr", "src_rowptr", "edge_ids_by_src", "source_node_order", "node_order")
+SEGMENT_TABLES = ("nodes", "begin", "end", "rowptr", "order")
+NUM_TABLES = 13
 
 
 @dataclass
@@ -31,8 +57,8 @@ class GraphTables:
     dst_rowptr: torch.Tensor
     src_rowptr: torch.Tensor
     edge_ids_by_src: torch.Tensor
-    node_order: torch.Tensor
     source_node_order: torch.Tensor
+    node_order: torch.Tensor
     num_nodes: int
 
     @property
@@ -40,138 +66,391 @@ class GraphTables:
         return int(self.src.numel())
 
 
-def graph_tables(graph):
-    return [getattr(graph, name) for name in GRAPH_TABLES]
+def graph_tables(graph) -> list:
+    """The 13 graph tables of ``graph`` in the reference's order."""
+    segments = graph.source_segments
+    seg = [None] * len(SEGMENT_TABLES) if segments is None else [getattr(segments, n) for n in SEGMENT_TABLES]
+    return [getattr(graph, name) for name in GRAPH_TABLES] + seg + [graph.node_tiers]
+
+
+def _tables(tables, num_nodes) -> GraphTables:
+    if len(tables) != NUM_TABLES:
+        raise ValueError(f"expected {NUM_TABLES} graph tables, got {len(tables)}")
+    for name, table in zip(GRAPH_TABLES, tables):
+        if table is None:
+            raise ValueError(f"graph table {name!r} is required")
+    return GraphTables(*tables[:len(GRAPH_TABLES)], num_nodes=int(num_nodes))
+
+
+# ---------------------------------------------------------------------------
+# Static configuration (the reference's encode_config / decode_config format)
+# ---------------------------------------------------------------------------
+
+def _encode(value):
+    if isinstance(value, tuple):
+        return {"tuple": [_encode(item) for item in value]}
+    if isinstance(value, torch.dtype):
+        return {"dtype": str(value).split(".")[-1]}
+    if isinstance(value, list):
+        return [_encode(item) for item in value]
+    if isinstance(value, dict):
+        return {key: _encode(item) for key, item in value.items()}
+    if value is None or isinstance(value, (str, bool, int, float)):
+        return value
+    raise TypeError(f"Unsupported operator configuration value: {type(value).__name__}")
+
+
+def _decode(value):
+    if isinstance(value, dict):
+        if set(value) == {"tuple"}:
+            return tuple(_decode(item) for item in value["tuple"])
+        if set(value) == {"dtype"}:
+            dtype = getattr(torch, value["dtype"], None)
+            if not isinstance(dtype, torch.dtype):
+                raise ValueError(f"Invalid operator dtype: {value['dtype']}")
+            return dtype
+        return {key: _decode(item) for key, item in value.items()}
+    if isinstance(value, list):
+        return [_decode(item) for item in value]
+    return value
 
 
 def operator_config(op) -> str:
     """Static configuration of a prepared convolution as a graph constant."""
-    meta = dict(op.meta)
-    meta["generated_specs"] = [dict(s, terms=[list(t) for t in s["terms"]]) for s in meta["generated_specs"]]
-    return json.dumps({"dtype": str(op.compute_dtype).split(".")[-1], "mode": op.mode, "meta": meta},
-                      sort_keys=True)
+    config = dict(mode=op.index_mode, dtype=op.compute_dtype, index_bits=op.index_bits,
+                  out_dim=int(op.meta["out_dim"]), l0_dim=int(getattr(op, "l0_dim", 0)),
+                  weight_mode="external", meta=op.meta)
+    return json.dumps(_encode(config), separators=(",", ":"))
+
+
+@lru_cache(maxsize=128)
+def decode_config(config: str) -> dict:
+    return _decode(json.loads(config))
 
 
 @lru_cache(maxsize=128)
 def restore_operator(config: str):
+    """Prepared operator of a configuration string (cached per string)."""
     from .uuu_conv import LunaTPUUUConv
     from .uvu_conv import LunaTPUVUConv
 
-    data = json.loads(config)
-    meta = data["meta"]
-    meta["generated_specs"] = [dict(s, terms=[tuple(t) for t in s["terms"]]) for s in meta["generated_specs"]]
-    cls = LunaTPUUUConv if data.get("mode") == "uuu_conv" else LunaTPUVUConv
-    return cls(meta, dtype=getattr(torch, data["dtype"]))
+    settings = decode_config(config)
+    mode = settings["mode"]
+    if mode not in ("uvu_conv", "uuu_conv"):
+        raise ValueError(f"unsupported convolution mode {mode!r}")
+    cls = LunaTPUUUConv if mode == "uuu_conv" else LunaTPUVUConv
+    return cls(dict(settings["meta"]), dtype=settings["dtype"], index_bits=int(settings.get("index_bits", 32)))
 
 
-@lru_cache(maxsize=128)
-def _static(config: str):
-    data = json.loads(config)
-    from .uvu_conv import l0_feature_layout
-
-    _, l0_dim = l0_feature_layout(data["meta"]["generated_specs"])
-    return data["meta"]["out_dim"], l0_dim
+def _out_dim(config: str) -> int:
+    return int(decode_config(config)["out_dim"])
 
 
-def _tables(tables, num_nodes):
-    return GraphTables(*tables, num_nodes=int(num_nodes))
+def _l0_dim(config: str) -> int:
+    return int(decode_config(config)["l0_dim"])
 
 
-def _register(prefix):
-    """Forward and backward dispatcher ops ``lunaeq_amd::<prefix>_conv_*`` with autograd."""
+# ---------------------------------------------------------------------------
+# Helpers
+# ---------------------------------------------------------------------------
 
-    @torch.library.custom_op(f"lunaeq_amd::{prefix}_conv_forward", mutates_args=(),
-                             schema="(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor[] tables, SymInt num_nodes, "
-                                    "bool return_l0, str config) -> (Tensor, Tensor?)")
-    def conv_forward(x, y, w, env, tables, num_nodes, return_l0, config):
-        out, l0 = restore_operator(config).launch_forward(x, y, w, _tables(tables, num_nodes), env, return_l0)
-        return out, l0
+def _present(t):
+    """None for an absent cotangent (None or 0-element), else a contiguous tensor."""
+    if t is None or t.numel() == 0:
+        return None
+    return t.contiguous()
 
-    @conv_forward.register_fake
-    def _conv_forward_fake(x, y, w, env, tables, num_nodes, return_l0, config):
-        out_dim, l0_dim = _static(config)
-        out = x.new_empty((num_nodes, out_dim))
-        return out, (y.new_empty((y.shape[0], l0_dim)) if return_l0 else None)
 
-    @torch.library.custom_op(f"lunaeq_amd::{prefix}_conv_backward", mutates_args=(),
-                             schema="(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor[] tables, "
-                                    "SymInt num_nodes, bool[] needs, str config) -> (Tensor?, Tensor?, Tensor?, Tensor?)")
-    def conv_backward(x, y, w, env, g, gl0, tables, num_nodes, needs, config):
-        return restore_operator(config).launch_backward(x, y, w, _tables(tables, num_nodes), g, env, gl0,
-                                                        tuple(needs))
+def _absent(like):
+    """The 0-element marker for a zero cotangent."""
+    return like.new_empty((0,))
 
-    @conv_backward.register_fake
-    def _conv_backward_fake(x, y, w, env, g, gl0, tables, num_nodes, needs, config):
-        return tuple(torch.empty_like(value) if need and value is not None else None
-                     for value, need in zip((x, y, w, env), needs))
 
-    def _forward_setup(ctx, inputs, output):
-        x, y, w, env, tables, num_nodes, return_l0, config = inputs
-        ctx.save_for_backward(x, y, w, env, *tables)
-        ctx.num_nodes, ctx.config, ctx.return_l0 = num_nodes, config, return_l0
-        ctx.table_count = len(tables)
-        ctx.set_materialize_grads(False)
+def _flat_env(env):
+    return None if env is None else env.reshape(-1).contiguous()
 
-    def _forward_backward(ctx, g, gl0):
-        x, y, w, env, *tables = ctx.saved_tensors
-        if g is None:
-            g = x.new_zeros((ctx.num_nodes, _static(ctx.config)[0]))
-        needs = list(ctx.needs_input_grad[:4])
-        gx, gy, gw, genv = conv_backward(x, y, w, env, g.contiguous(),
-                                         None if gl0 is None else gl0.contiguous(),
-                                         list(tables), ctx.num_nodes, needs, ctx.config)
-        return gx, gy, gw, genv, [None] * ctx.table_count, None, None, None
 
-    def _backward_setup(ctx, inputs, output):
-        x, y, w, env, g, gl0, tables, num_nodes, needs, config = inputs
-        ctx.save_for_backward(x, y, w, env, g, gl0, *tables)
-        ctx.num_nodes, ctx.config = num_nodes, config
-        ctx.table_count = len(tables)
-        ctx.set_materialize_grads(False)
-
-    def _backward_backward(ctx, rx, ry, rw, renv):
-        x, y, w, env, g, gl0, *tables = ctx.saved_tensors
-        need = ctx.needs_input_grad  # x, y, w, env, g, gl0, tables, num_nodes, needs, config
-        want_l0 = gl0 is not None
-        args = [x, y, w, env]
-        dirs = [None if r is None else r.contiguous() for r in (rx, ry, rw)]
-        dirs.append(None if (renv is None or env is None) else renv.contiguous())
-        grads = [None] * 4
-        hg = hl0 = None
-        for slot, direction in enumerate(dirs):
-            if direction is None:
-                continue
-            sub = list(args)
-            sub[slot] = direction
-            # Along a weight direction only the weighted paths vary.
-            config = restore_operator(ctx.config).weight_linear().torch_config if slot == 2 else ctx.config
-            scalar = want_l0 and slot != 3
-            if need[4] or (need[5] and scalar):
-                out, l0 = conv_forward(*sub, list(tables), ctx.num_nodes, scalar, config)
-                hg = _add(hg, out)
-                if scalar:
-                    hl0 = _add(hl0, l0)
-            wanted = [bool(need[o]) and o != slot and args[o] is not None for o in range(4)]
-            if any(wanted):
-                parts = conv_backward(*sub, g, gl0 if slot != 3 else None, list(tables), ctx.num_nodes, wanted,
-                                      config)
-                for o in range(4):
-                    if wanted[o] and parts[o] is not None:
-                        grads[o] = _add(grads[o], parts[o])
-        return (*grads, hg if need[4] else None, hl0 if need[5] else None, [None] * ctx.table_count, None, None,
-                None)
-
-    conv_forward.register_autograd(_forward_backward, setup_context=_forward_setup)
-    conv_backward.register_autograd(_backward_backward, setup_context=_backward_setup)
-    return conv_forward, conv_backward
+def _like_env(value, env):
+    return None if value is None or env is None else value.reshape(env.shape)
 
 
 def _add(a, b):
     return b if a is None else (a if b is None else a + b)
 
 
-conv_forward, conv_backward = _register("uvu")
-uuu_conv_forward, uuu_conv_backward = _register("uuu")
+def _empty_like(value):
+    return torch.empty_like(value, memory_format=torch.contiguous_format)
 
 
-__all__ = ["conv_forward", "conv_backward", "uuu_conv_forward", "uuu_conv_backward", "operator_config", "restore_operator", "graph_tables"]
+def _launch_backward(op, x, y, w, env, g, gl0, graph, needs):
+    gx, gy, gw, genv = op.launch_backward(x, y, w, graph, g, env, gl0, tuple(bool(n) for n in needs))
+    return gx, gy, gw, genv
+
+
+def _double(op, x, y, w, env, g, gl0, dirs, graph, needs):
+    """Second-order terms of <r, backward(x, y, w, env, g, gl0)>.
+
+    dirs = (rx, ry, rw, re), None where zero.  Returns (hx, hy, hw, he, hg, hl0):
+    hg = sum_i F(args with a_i -> r_i); h_j = sum_{i != j} B_j(g; args with a_i -> r_i).
+    The scalar features do not depend on env, so an env direction moves only hg.
+    """
+    args = [x, y, w, env]
+    grads = [None] * 4
+    hg = hl0 = None
+    want_l0 = gl0 is not None
+    for slot, direction in enumerate(dirs):
+        if direction is None or (slot == 3 and env is None):
+            continue
+        sub = list(args)
+        sub[slot] = direction
+        sop = op.weight_linear() if slot == 2 else op
+        scalar = want_l0 and slot != 3
+        if needs[4] or (needs[5] and scalar):
+            out, l0 = sop.launch_forward(sub[0], sub[1], sub[2], graph, sub[3], scalar)
+            hg = _add(hg, out)
+            if scalar:
+                hl0 = _add(hl0, l0)
+        wanted = [bool(needs[o]) and o != slot and args[o] is not None for o in range(4)]
+        if any(wanted):
+            parts = _launch_backward(sop, *sub, g, gl0 if slot != 3 else None, graph, wanted)
+            for o in range(4):
+                if wanted[o] and parts[o] is not None:
+                    grads[o] = _add(grads[o], parts[o])
+    return grads[0], grads[1], grads[2], grads[3], hg, hl0
+
+
+def _zero_if_none(value, template, need):
+    if not need or template is None:
+        return None
+    return torch.zeros_like(template, memory_format=torch.contiguous_format) if value is None else value
+
+
+# ---------------------------------------------------------------------------
+# Registration
+# ---------------------------------------------------------------------------
+
+def _register(prefix):
+    name = f"lunatp::{prefix}_conv"
+
+    @torch.library.custom_op(f"{name}_forward", mutates_args=(),
+                             schema="(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor?[] tables, SymInt num_nodes, "
+                                    "bool return_l0, str config) -> (Tensor, Tensor?)")
+    def conv_forward(x, y, w, env, tables, num_nodes, return_l0, config):
+        op = restore_operator(config)
+        out, l0 = op.launch_forward(x.contiguous(), y.contiguous(), w.contiguous(), _tables(tables, num_nodes),
+                                    _flat_env(env), bool(return_l0))
+        return out, l0
+
+    @conv_forward.register_fake
+    def _forward_fake(x, y, w, env, tables, num_nodes, return_l0, config):
+        out = x.new_empty((num_nodes, _out_dim(config)))
+        return out, (y.new_empty((y.shape[0], _l0_dim(config))) if return_l0 else None)
+
+    @torch.library.custom_op(f"{name}_backward", mutates_args=(),
+                             schema="(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor?[] tables, "
+                                    "SymInt num_nodes, bool[] needs, str config) -> (Tensor?, Tensor?, Tensor?, Tensor?)")
+    def conv_backward(x, y, w, env, g, gl0, tables, num_nodes, needs, config):
+        op = restore_operator(config)
+        gx, gy, gw, ge = _launch_backward(op, x.contiguous(), y.contiguous(), w.contiguous(), _flat_env(env),
+                                          g.contiguous(), _present(gl0), _tables(tables, num_nodes), needs)
+        return gx, gy, gw, _like_env(ge, env)
+
+    @conv_backward.register_fake
+    def _backward_fake(x, y, w, env, g, gl0, tables, num_nodes, needs, config):
+        return tuple(_empty_like(v) if need and v is not None else None for v, need in zip((x, y, w, env), needs))
+
+    @torch.library.custom_op(f"{name}_double_backward", mutates_args=(),
+                             schema="(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor rx, "
+                                    "Tensor ry, Tensor rw, Tensor? re, Tensor?[] tables, SymInt num_nodes, bool[] needs, "
+                                    "str config) -> (Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, Tensor?)")
+    def conv_double_backward(x, y, w, env, g, gl0, rx, ry, rw, re, tables, num_nodes, needs, config):
+        op = restore_operator(config)
+        flat = _flat_env(env)
+        re = _present(re)
+        result = _double(op, x.contiguous(), y.contiguous(), w.contiguous(), flat, g.contiguous(), _present(gl0),
+                         (_present(rx), _present(ry), _present(rw), None if re is None else re.reshape(-1)),
+                         _tables(tables, num_nodes), needs)
+        hx, hy, hw, he, hg, hl0 = result
+        he = _like_env(he, env)
+        # Requested outputs exist even when every contributing direction was zero.
+        templates = (x, y, w, env, g, gl0)
+        return tuple(_zero_if_none(v, t, need) for v, t, need in zip((hx, hy, hw, he, hg, hl0), templates, needs))
+
+    @conv_double_backward.register_fake
+    def _double_fake(x, y, w, env, g, gl0, rx, ry, rw, re, tables, num_nodes, needs, config):
+        return tuple(_empty_like(v) if need and v is not None else None
+                     for v, need in zip((x, y, w, env, g, gl0), needs))
+
+    @torch.library.custom_op(f"{name}_triple_backward", mutates_args=(),
+                             schema="(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor rx, "
+                                    "Tensor ry, Tensor rw, Tensor? re, Tensor sx, Tensor sy, Tensor sw, Tensor sg, "
+                                    "Tensor? se, Tensor? sl0, Tensor?[] tables, SymInt num_nodes, bool[] needs, "
+                                    "str config) -> (Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, "
+                                    "Tensor?, Tensor?, Tensor?)")
+    def conv_triple_backward(x, y, w, env, g, gl0, rx, ry, rw, re, sx, sy, sw, sg, se, sl0, tables, num_nodes,
+                             needs, config):
+        return _triple(restore_operator(config), x, y, w, env, g, gl0, (rx, ry, rw, re), (sx, sy, sw, se, sg, sl0),
+                       _tables(tables, num_nodes), needs)
+
+    @conv_triple_backward.register_fake
+    def _triple_fake(x, y, w, env, g, gl0, rx, ry, rw, re, sx, sy, sw, sg, se, sl0, tables, num_nodes, needs,
+                     config):
+        return tuple(_empty_like(v) if need and v is not None else None
+                     for v, need in zip((x, y, w, env, g, gl0, rx, ry, rw, re), needs))
+
+    # ---- autograd ----
+
+    def _forward_setup(ctx, inputs, output):
+        x, y, w, env, tables, num_nodes, _, config = inputs
+        ctx.save_for_backward(x, y, w, env, *tables)
+        ctx.num_nodes, ctx.config, ctx.table_count = num_nodes, config, len(tables)
+        ctx.set_materialize_grads(False)
+
+    def _forward_backward(ctx, g, gl0):
+        x, y, w, env, *tables = ctx.saved_tensors
+        if g is None:
+            g = x.new_zeros((ctx.num_nodes, _out_dim(ctx.config)))
+        result = conv_backward(x, y, w, env, g.contiguous(), None if gl0 is None else gl0.contiguous(),
+                               list(tables), ctx.num_nodes, list(ctx.needs_input_grad[:4]), ctx.config)
+        return *result, [None] * ctx.table_count, None, None, None
+
+    def _backward_setup(ctx, inputs, output):
+        tables = inputs[-4]
+        ctx.save_for_backward(*inputs[:-4], *tables)
+        ctx.num_nodes, ctx.config, ctx.table_count = inputs[-3], inputs[-1], len(tables)
+        ctx.set_materialize_grads(False)
+
+    def _backward_backward(ctx, rx, ry, rw, re):
+        x, y, w, env, g, gl0, *tables = ctx.saved_tensors
+        rx, ry, rw = (_absent(t) if r is None else r.contiguous() for r, t in zip((rx, ry, rw), (x, y, w)))
+        re = None if (re is None or env is None) else re.contiguous()
+        result = conv_double_backward(x, y, w, env, g, gl0, rx, ry, rw, re, list(tables), ctx.num_nodes,
+                                      list(ctx.needs_input_grad[:6]), ctx.config)
+        return *result, [None] * ctx.table_count, None, None, None
+
+    def _double_backward_backward(ctx, sx, sy, sw, se, sg, sl0):
+        x, y, w, env, g, gl0, rx, ry, rw, re, *tables = ctx.saved_tensors
+        sx, sy, sw, sg = (_absent(t) if s is None else s.contiguous() for s, t in zip((sx, sy, sw, sg), (x, y, w, g)))
+        se = None if (se is None or env is None) else se.contiguous()
+        sl0 = None if (sl0 is None or gl0 is None) else sl0.contiguous()
+        result = conv_triple_backward(x, y, w, env, g, gl0, rx, ry, rw, re, sx, sy, sw, sg, se, sl0, list(tables),
+                                      ctx.num_nodes, list(ctx.needs_input_grad[:10]), ctx.config)
+        return *result, [None] * ctx.table_count, None, None, None
+
+    conv_forward.register_autograd(_forward_backward, setup_context=_forward_setup)
+    conv_backward.register_autograd(_backward_backward, setup_context=_backward_setup)
+    conv_double_backward.register_autograd(_double_backward_backward, setup_context=_backward_setup)
+    return conv_forward, conv_backward, conv_double_backward, conv_triple_backward
+
+
+def _triple(op, x, y, w, env, g, gl0, rs, ss, graph, needs):
+    """Gradients of T = <s, double_backward(a, G; r)> w.r.t. its ten inputs.
+
+    With a = (x, y, w, env), seeds G = (g, gl0) and F the (multilinear) forward,
+    the double backward is the gradient of sum_j <G, F(a with a_j -> r_j)>, so
+
+      T = sum_{i != j} <G, F(a; a_j -> r_j, a_i -> s_i)> + sum_j <sG, F(a; a_j -> r_j)>
+
+    with s = (sx, sy, sw, se) and sG = (sg, sl0).  Its gradients are again
+    forward and backward kernel calls with substituted arguments:
+
+      dG   = sum_{i != j} F(a; a_j -> r_j, a_i -> s_i)
+      dr_j = sum_{i != j} B_j(a; a_i -> s_i; G) + B_j(a; sG)
+      da_k = sum_{i != j; i, j != k} B_k(a; a_j -> r_j, a_i -> s_i; G) + sum_{j != k} B_k(a; a_j -> r_j; sG)
+
+    Any term with env substituted has no scalar-feature part (the l0 features
+    do not depend on env), and any term with w substituted runs the operator's
+    weight-linear part.
+    """
+    flat = _flat_env(env)
+    args = [x.contiguous(), y.contiguous(), w.contiguous(), flat]
+    g = g.contiguous()
+    gl0 = _present(gl0)
+    r = [_present(t) for t in rs]
+    s = [_present(t) for t in ss[:4]]
+    if env is None:
+        r[3] = s[3] = None
+    r[3] = None if r[3] is None else r[3].reshape(-1)
+    s[3] = None if s[3] is None else s[3].reshape(-1)
+    sg, sl0 = _present(ss[4]), _present(ss[5])
+    if gl0 is None:
+        sl0 = None
+    seed_present = sg is not None or sl0 is not None
+    if seed_present and sg is None:
+        sg = g.new_zeros(g.shape)
+    grads = [None] * 10  # x, y, w, env, g, gl0, rx, ry, rw, re
+
+    def call(subs, seed, seed_l0, want_k, want_out):
+        """Forward (for dG) and backward B_k (k in want_k) at a with `subs` substituted."""
+        sub = list(args)
+        for slot, value in subs.items():
+            sub[slot] = value
+        sop = op.weight_linear() if 2 in subs else op
+        env_sub = 3 in subs
+        scalar = gl0 is not None and not env_sub
+        if want_out and (needs[4] or (needs[5] and scalar)):
+            out, l0 = sop.launch_forward(sub[0], sub[1], sub[2], graph, sub[3], scalar)
+            grads[4] = _add(grads[4], out)
+            if scalar:
+                grads[5] = _add(grads[5], l0)
+        wanted = [k in want_k and k not in subs and args[k] is not None for k in range(4)]
+        if any(wanted):
+            parts = _launch_backward(sop, *sub, seed, None if env_sub else seed_l0, graph, wanted)
+            return parts
+        return (None,) * 4
+
+    for j in range(4):
+        for i in range(4):
+            if i == j or r[j] is None or s[i] is None:
+                continue
+            # dG and da_k for k outside {i, j}.
+            want = {k for k in range(4) if k not in (i, j) and needs[k]}
+            parts = call({j: r[j], i: s[i]}, g, gl0, want, True)
+            for k in want:
+                grads[k] = _add(grads[k], parts[k])
+    for i in range(4):
+        if s[i] is None:
+            continue
+        # dr_j = B_j(a; a_i -> s_i; G) for j != i.
+        want = {j for j in range(4) if j != i and needs[6 + j]}
+        parts = call({i: s[i]}, g, gl0, want, False)
+        for j in want:
+            grads[6 + j] = _add(grads[6 + j], parts[j])
+    if seed_present:
+        # dr_j += B_j(a; sG)
+        want = {j for j in range(4) if needs[6 + j]}
+        parts = call({}, sg, sl0, want, False)
+        for j in want:
+            grads[6 + j] = _add(grads[6 + j], parts[j])
+        # da_k += B_k(a; a_j -> r_j; sG) for k != j
+        for j in range(4):
+            if r[j] is None:
+                continue
+            want = {k for k in range(4) if k != j and needs[k]}
+            parts = call({j: r[j]}, sg, sl0, want, False)
+            for k in want:
+                grads[k] = _add(grads[k], parts[k])
+    shapes = [x.shape, y.shape, w.shape, None if env is None else env.shape, g.shape,
+              None if gl0 is None else gl0.shape, x.shape, y.shape, w.shape, None if env is None else env.shape]
+    result = []
+    for n, value in enumerate(grads):
+        if not needs[n] or shapes[n] is None or (n == 5 and gl0 is None):
+            result.append(None)
+            continue
+        if value is None:
+            value = torch.zeros(shapes[n], dtype=x.dtype, device=x.device)
+        result.append(value.reshape(shapes[n]).contiguous())
+    return tuple(result)
+
+
+(uvu_conv_forward, uvu_conv_backward, uvu_conv_double_backward,
+ uvu_conv_triple_backward) = _register("uvu")
+(uuu_conv_forward, uuu_conv_backward, uuu_conv_double_backward,
+ uuu_conv_triple_backward) = _register("uuu")
+
+# Earlier names of the first-order UVU ops in this package.
+conv_forward, conv_backward = uvu_conv_forward, uvu_conv_backward
+
+__all__ = ["uvu_conv_forward", "uvu_conv_backward", "uvu_conv_double_backward", "uvu_conv_triple_backward",
+           "uuu_conv_forward", "uuu_conv_backward", "uuu_conv_double_backward", "uuu_conv_triple_backward",
+           "operator_config", "restore_operator", "graph_tables", "decode_config", "GRAPH_TABLES", "NUM_TABLES"]

@@ -315,7 +315,7 @@ def lunatp_uuu_conv_func(op, x, edge_attr, weight=None, *, graph: LunaTPGraph, e
     if torch.compiler.is_compiling():
         from . import ops
 
-        out, l0 = torch.ops.lunaeq_amd.uuu_conv_forward(
+        out, l0 = torch.ops.lunatp.uuu_conv_forward.default(
             x, edge_attr, weight, env, ops.graph_tables(graph), graph.num_nodes, bool(return_l0_feat),
             op.torch_config)
         return (out, l0) if return_l0_feat else out

@@ -440,7 +440,7 @@ def lunatp_uvu_conv_func(op, x, edge_attr, weight, *, graph: LunaTPGraph, env=No
     if torch.compiler.is_compiling():
         from . import ops
 
-        out, l0 = torch.ops.lunaeq_amd.uvu_conv_forward(
+        out, l0 = torch.ops.lunatp.uvu_conv_forward.default(
             x, edge_attr, weight, env, ops.graph_tables(graph), graph.num_nodes, bool(return_l0_feat),
             op.torch_config)
         return (out, l0) if return_l0_feat else out

@@ -188,7 +188,7 @@ class LunaTPUVWConv:
         if torch.compiler.is_compiling():
             from . import ops
 
-            out, _ = torch.ops.lunaeq_amd.uvu_conv_forward(x, y, ones, env, ops.graph_tables(graph),
+            out, _ = torch.ops.lunatp.uvu_conv_forward.default(x, y, ones, env, ops.graph_tables(graph),
                                                             graph.num_nodes, False, self.agg.torch_config)
             return out
         return ConvForward.apply(self.agg, graph, False, x, y, ones, env)

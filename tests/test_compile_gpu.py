@@ -30,10 +30,10 @@ def test_opcheck_forward_and_backward():
     conv, graph, x, y, w = problem()
     tables = ops.graph_tables(graph)
     config = conv.op.torch_config
-    torch.library.opcheck(torch.ops.lunaeq_amd.uvu_conv_forward.default,
+    torch.library.opcheck(torch.ops.lunatp.uvu_conv_forward.default,
                           (x, y, w, None, tables, graph.num_nodes, False, config))
     g = torch.randn(graph.num_nodes, conv.irreps_out.dim, device=DEV)
-    torch.library.opcheck(torch.ops.lunaeq_amd.uvu_conv_backward.default,
+    torch.library.opcheck(torch.ops.lunatp.uvu_conv_backward.default,
                           (x.detach(), y.detach(), w.detach(), None, g, None, tables, graph.num_nodes,
                            [True, True, True, False], config))
 
@@ -62,7 +62,7 @@ def test_dispatcher_ops_differentiate_to_second_order():
     """Outside compilation the operators' own autograd composes second order."""
     conv, graph, x, y, w = problem(seed=3)
     tables = ops.graph_tables(graph)
-    out, _ = torch.ops.lunaeq_amd.uvu_conv_forward(x, y, w, None, tables, graph.num_nodes, False,
+    out, _ = torch.ops.lunatp.uvu_conv_forward.default(x, y, w, None, tables, graph.num_nodes, False,
                                                    conv.op.torch_config)
     eager = conv(x, y, w, graph=graph)
     assert_close(out, eager.double(), torch.float32, "op forward")
@@ -97,8 +97,8 @@ def other_mode_problem(mode, seed=0, nodes=10, edges=40):
 
 @pytest.mark.parametrize("mode", ["uuu", "uvw"])
 def test_compiled_uuu_and_uvw_match_eager(mode):
-    """UUU runs through lunaeq_amd::uuu_conv_*, the shared-weight UVW aggregation through
-    lunaeq_amd::uvu_conv_* plus library GEMMs; compiled forward and first order equal eager."""
+    """UUU runs through lunatp::uuu_conv_*, the shared-weight UVW aggregation through
+    lunatp::uvu_conv_* plus library GEMMs; compiled forward and first order equal eager."""
     conv, graph, x, y, w = other_mode_problem(mode)
 
     def layer(a, b, c):
@@ -118,10 +118,10 @@ def test_opcheck_uuu():
     conv, graph, x, y, w = other_mode_problem("uuu", seed=2)
     tables = ops.graph_tables(graph)
     config = conv.op.torch_config
-    torch.library.opcheck(torch.ops.lunaeq_amd.uuu_conv_forward.default,
+    torch.library.opcheck(torch.ops.lunatp.uuu_conv_forward.default,
                           (x, y, w, None, tables, graph.num_nodes, False, config))
     g = torch.randn(graph.num_nodes, conv.irreps_out.dim, device=DEV)
-    torch.library.opcheck(torch.ops.lunaeq_amd.uuu_conv_backward.default,
+    torch.library.opcheck(torch.ops.lunatp.uuu_conv_backward.default,
                           (x.detach(), y.detach(), w.detach(), None, g, None, tables, graph.num_nodes,
                            [True, True, True, False], config))
 
@@ -143,7 +143,7 @@ def test_uuu_dispatcher_ops_second_order_with_unweighted_paths():
     x = torch.randn(nodes, a.dim, generator=gen).to(DEV).requires_grad_()
     y = torch.randn(edges, a.dim, generator=gen).to(DEV).requires_grad_()
     w = torch.randn(edges, conv.weight_numel, generator=gen).to(DEV).requires_grad_()
-    out, _ = torch.ops.lunaeq_amd.uuu_conv_forward(x, y, w, None, ops.graph_tables(graph), nodes, False,
+    out, _ = torch.ops.lunatp.uuu_conv_forward.default(x, y, w, None, ops.graph_tables(graph), nodes, False,
                                                    conv.op.torch_config)
     eager = conv(x, y, w, graph=graph)
     assert_close(out, eager.double(), torch.float32, "uuu op forward")
@@ -153,3 +153,105 @@ def test_uuu_dispatcher_ops_second_order_with_unweighted_paths():
     dirs = [torch.randn_like(t) for t in first_e]
     for a_, b_ in zip(torch.autograd.grad(first_o, (x, y, w), dirs), torch.autograd.grad(first_e, (x, y, w), dirs)):
         assert_close(a_, b_.double(), torch.float32, "uuu op second order")
+
+
+def _opcheck_all_orders(conv, graph, x, y, w, env=None, gl0=False):
+    prefix = conv.op.index_mode.split("_")[0]
+    ns = torch.ops.lunatp
+    tables = ops.graph_tables(graph)
+    assert len(tables) == 13
+    config = conv.op.torch_config
+    x, y, w = x.detach(), y.detach(), w.detach()
+    n = graph.num_nodes
+    g = torch.randn(n, conv.irreps_out.dim, device=DEV, dtype=x.dtype)
+    l0 = torch.randn(y.shape[0], conv.op.l0_dim, device=DEV, dtype=x.dtype) if gl0 else None
+    rx, ry, rw = torch.randn_like(x), torch.randn_like(y), torch.randn_like(w)
+    re = None if env is None else torch.randn_like(env)
+    sx, sy, sw, sg = torch.randn_like(x), torch.randn_like(y), torch.randn_like(w), torch.randn_like(g)
+    se = None if env is None else torch.randn_like(env)
+    sl0 = None if l0 is None else torch.randn_like(l0)
+    torch.library.opcheck(getattr(ns, f"{prefix}_conv_forward").default, (x, y, w, env, tables, n, gl0, config))
+    torch.library.opcheck(getattr(ns, f"{prefix}_conv_backward").default,
+                          (x, y, w, env, g, l0, tables, n, [True, True, True, env is not None], config))
+    torch.library.opcheck(getattr(ns, f"{prefix}_conv_double_backward").default,
+                          (x, y, w, env, g, l0, rx, ry, rw, re, tables, n,
+                           [True, True, True, env is not None, True, gl0], config))
+    torch.library.opcheck(getattr(ns, f"{prefix}_conv_triple_backward").default,
+                          (x, y, w, env, g, l0, rx, ry, rw, re, sx, sy, sw, sg, se, sl0, tables, n,
+                           [True, True, True, env is not None, True, gl0, True, True, True, env is not None],
+                           config))
+
+
+def test_opcheck_reference_ops_all_orders():
+    """lunatp::uvu_conv_{forward,backward,double_backward,triple_backward} with the reference's
+    schemas and 13-entry table list (src/lunatp/uvu_conv/interface.py:18-89, :186-192)."""
+    conv, graph, x, y, w = problem(seed=7)
+    env = torch.randn(y.shape[0], 1, device=DEV)
+    _opcheck_all_orders(conv, graph, x, y, w)
+    _opcheck_all_orders(conv, graph, x, y, w, env=env, gl0=True)
+
+
+def test_opcheck_reference_uuu_ops_all_orders():
+    conv, graph, x, y, w = other_mode_problem("uuu", seed=8)
+    _opcheck_all_orders(conv, graph, x, y, w, env=torch.randn(y.shape[0], device=DEV), gl0=True)
+
+
+@pytest.mark.parametrize("with_env", [False, True])
+def test_reference_table_list_third_order(with_env):
+    """Calling the forward op as the reference's compiled path does (13 tables, env [E, 1],
+    return_l0) differentiates to third order through the double/triple ops, matching the
+    module's own autograd."""
+    conv, graph, x, y, w = problem(dtype=torch.float64, seed=11)
+    g0 = torch.Generator().manual_seed(12)
+    env = None
+    if with_env:
+        env = torch.randn(y.shape[0], 1, generator=g0, dtype=torch.float64).to(DEV).requires_grad_()
+    segments = graph.source_segments
+    tables = [graph.src, graph.dst, graph.dst_rowptr, graph.src_rowptr, graph.edge_ids_by_src,
+              graph.source_node_order, graph.node_order, segments.nodes, segments.begin, segments.end,
+              segments.rowptr, segments.order, graph.node_tiers]
+    out, l0 = torch.ops.lunatp.uvu_conv_forward.default(x, y, w, env, tables, graph.num_nodes, True,
+                                                        conv.op.torch_config)
+    ref_out, ref_l0 = conv(x, y, w, graph=graph, env=env, return_l0_feat=True)
+    assert_close(out, ref_out, torch.float64, "op forward")
+    assert_close(l0, ref_l0, torch.float64, "op l0")
+    inputs = (x, y, w) + ((env,) if with_env else ())
+
+    def scalar(o, l):
+        return (o * torch.sin(o)).sum() + (l ** 3).sum()
+
+    first_o = torch.autograd.grad(scalar(out, l0), inputs, create_graph=True)
+    first_e = torch.autograd.grad(scalar(ref_out, ref_l0), inputs, create_graph=True)
+    dirs = [torch.randn(t.shape, generator=g0, dtype=t.dtype).to(DEV) for t in first_e]
+    second_o = torch.autograd.grad(first_o, inputs, dirs, create_graph=True)
+    second_e = torch.autograd.grad(first_e, inputs, dirs, create_graph=True)
+    for a, b in zip(first_o + second_o, first_e + second_e):
+        assert_close(a, b, torch.float64, "op first/second order")
+    dirs2 = [torch.randn(t.shape, generator=g0, dtype=t.dtype).to(DEV) for t in second_e]
+    third_o = torch.autograd.grad(second_o, inputs, dirs2, allow_unused=True)
+    third_e = torch.autograd.grad(second_e, inputs, dirs2, allow_unused=True)
+    for a, b in zip(third_o, third_e):
+        if b is None:
+            assert a is None or float(a.abs().max()) == 0.0
+            continue
+        assert_close(a, b, torch.float64, "op third order")
+
+
+def test_double_backward_op_skips_absent_cotangents():
+    """Materialised zero cotangents (as the reference passes them) and 0-element markers give
+    the same double-backward result."""
+    conv, graph, x, y, w = problem(seed=13)
+    tables = ops.graph_tables(graph)
+    x, y, w = x.detach(), y.detach(), w.detach()
+    g = torch.randn(graph.num_nodes, conv.irreps_out.dim, device=DEV)
+    ry = torch.randn_like(y)
+    needs = [True, True, True, False, True, False]
+    op = torch.ops.lunatp.uvu_conv_double_backward.default
+    full = op(x, y, w, None, g, None, torch.zeros_like(x), ry, torch.zeros_like(w), None, tables,
+              graph.num_nodes, needs, conv.op.torch_config)
+    marker = op(x, y, w, None, g, None, x.new_empty(0), ry, w.new_empty(0), None, tables, graph.num_nodes,
+                needs, conv.op.torch_config)
+    for a, b in zip(full, marker):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert_close(a, b.double(), torch.float32, "zero vs marker")

@@ -1,0 +1,123 @@
+"""The dispatcher ops carry the reference's names and schemas
+(src/lunatp/uvu_conv/interface.py:18-89, src/lunatp/uuu_conv/interface.py:15-95)
+and its static-configuration format (src/utils/operator_config.py,
+src/lunatp/interface.py:57-73).  CPU only: schemas, config round trips and fake
+(meta) shape inference."""
+
+import json
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+import lunaequivariance_amd as lunaeq
+from lunaequivariance_amd import ops
+from lunaequivariance_amd.workloads import mace_irreps
+
+SCHEMAS = {
+    "forward": "(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor?[] tables, SymInt num_nodes, bool return_l0, "
+               "str config) -> (Tensor, Tensor?)",
+    "backward": "(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor?[] tables, "
+                "SymInt num_nodes, bool[] needs, str config) -> (Tensor?, Tensor?, Tensor?, Tensor?)",
+    "double_backward": "(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor rx, Tensor ry, "
+                       "Tensor rw, Tensor? re, Tensor?[] tables, SymInt num_nodes, bool[] needs, str config) -> "
+                       "(Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, Tensor?)",
+    "triple_backward": "(Tensor x, Tensor y, Tensor w, Tensor? env, Tensor g, Tensor? gl0, Tensor rx, Tensor ry, "
+                       "Tensor rw, Tensor? re, Tensor sx, Tensor sy, Tensor sw, Tensor sg, Tensor? se, Tensor? sl0, "
+                       "Tensor?[] tables, SymInt num_nodes, bool[] needs, str config) -> (Tensor?, Tensor?, Tensor?, "
+                       "Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, Tensor?, Tensor?)",
+}
+
+
+def _normalise(schema: str) -> str:
+    return " ".join(schema.split())
+
+
+@pytest.mark.parametrize("mode", ["uvu", "uuu"])
+@pytest.mark.parametrize("kind", sorted(SCHEMAS))
+def test_schema_matches_reference(mode, kind):
+    op = getattr(torch.ops.lunatp, f"{mode}_conv_{kind}").default
+    text = str(op._schema)
+    assert text.startswith(f"lunatp::{mode}_conv_{kind}(")
+    assert _normalise(text[text.index("("):]) == _normalise(SCHEMAS[kind])
+
+
+def conv_of(channels=4, lmax=2, dtype=torch.float32):
+    in1, sh, out, ins = mace_irreps(channels, lmax)
+    return lunaeq.TensorProductConv(in1, sh, out, ins, internal_weights=False, shared_weights=False, dtype=dtype)
+
+
+def test_config_format_and_round_trip():
+    conv = conv_of(dtype=torch.float64)
+    config = conv.op.torch_config
+    data = json.loads(config)
+    # The reference's keys and tagging: dtypes as {"dtype": name}, tuples as {"tuple": [...]}.
+    assert set(data) == {"mode", "dtype", "index_bits", "out_dim", "l0_dim", "weight_mode", "meta"}
+    assert data["mode"] == "uvu_conv" and data["dtype"] == {"dtype": "float64"} and data["index_bits"] == 32
+    assert data["weight_mode"] == "external" and data["out_dim"] == conv.irreps_out.dim
+    term = data["meta"]["generated_specs"][0]["terms"][0]
+    assert set(term) == {"tuple"} and len(term["tuple"]) == 4
+    assert "," in config and ", " not in config  # compact separators
+    op = ops.restore_operator(config)
+    assert op.compute_dtype == torch.float64 and op.meta == conv.op.meta
+    assert ops.operator_config(op) == config
+
+
+def test_config_rejects_unknown_mode_and_dtype():
+    config = json.loads(conv_of().op.torch_config)
+    bad = dict(config, mode="so2_conv")
+    with pytest.raises(ValueError):
+        ops.restore_operator(json.dumps(bad))
+    with pytest.raises(ValueError):
+        ops.decode_config(json.dumps(dict(config, dtype={"dtype": "not_a_dtype"})))
+
+
+def test_graph_tables_reference_order():
+    conv = conv_of()
+    src = torch.tensor([1, 2, 0, 3, 3, 1])
+    dst = torch.tensor([0, 0, 1, 1, 2, 3])
+    graph = conv.create_graph(src, dst, 4)
+    tables = ops.graph_tables(graph)
+    seg = graph.source_segments
+    expected = [graph.src, graph.dst, graph.dst_rowptr, graph.src_rowptr, graph.edge_ids_by_src,
+                graph.source_node_order, graph.node_order, seg.nodes, seg.begin, seg.end, seg.rowptr,
+                seg.order, graph.node_tiers]
+    assert len(tables) == ops.NUM_TABLES == 13
+    assert all(a is b for a, b in zip(tables, expected))
+    with pytest.raises(ValueError):
+        ops._tables(tables[:7], 4)
+
+
+@pytest.mark.parametrize("env_shape", [None, (1,), ()])
+def test_fake_kernels_give_reference_shapes(env_shape):
+    conv = conv_of()
+    N, E = 5, 11
+    config = conv.op.torch_config
+    l0_dim = conv.op.l0_dim
+    with FakeTensorMode():
+        x = torch.empty(N, conv.irreps_in1.dim)
+        y = torch.empty(E, conv.irreps_in2.dim)
+        w = torch.empty(E, conv.weight_numel)
+        g = torch.empty(N, conv.irreps_out.dim)
+        env = None if env_shape is None else torch.empty((E,) + env_shape)
+        gl0 = torch.empty(E, l0_dim)
+        tables = [torch.empty(E, dtype=torch.int32)] * 13
+        out, l0 = torch.ops.lunatp.uvu_conv_forward.default(x, y, w, env, tables, N, True, config)
+        assert out.shape == (N, conv.irreps_out.dim) and l0.shape == (E, l0_dim)
+        out, l0 = torch.ops.lunatp.uvu_conv_forward.default(x, y, w, env, tables, N, False, config)
+        assert l0 is None
+        has_env = env is not None
+        grads = torch.ops.lunatp.uvu_conv_backward.default(x, y, w, env, g, gl0, tables, N,
+                                                           [True, False, True, has_env], config)
+        assert grads[0].shape == x.shape and grads[1] is None and grads[2].shape == w.shape
+        assert (grads[3] is None) == (not has_env)
+        if has_env:
+            assert grads[3].shape == env.shape
+        double = torch.ops.lunatp.uvu_conv_double_backward.default(
+            x, y, w, env, g, gl0, x, y, w, env, tables, N, [True, True, True, has_env, True, True], config)
+        assert [None if t is None else tuple(t.shape) for t in double] == \
+            [tuple(x.shape), tuple(y.shape), tuple(w.shape), tuple(env.shape) if has_env else None,
+             tuple(g.shape), tuple(gl0.shape)]
+        triple = torch.ops.lunatp.uvu_conv_triple_backward.default(
+            x, y, w, env, g, gl0, x, y, w, env, x, y, w, g, env, gl0, tables, N, [True] * 10, config)
+        assert len(triple) == 10 and triple[6].shape == x.shape and triple[4].shape == g.shape

@@ -219,7 +219,7 @@ def test_prebuilt_metadata_and_compile_op():
     graph = conv.create_graph(src.to(DEV), dst.to(DEV), 6)
     a = conv(x, y, w, graph=graph)
     b = lunaeq.tensor_product_conv(x, y, w, graph=graph, config=prepared)
-    c, _ = torch.ops.lunaeq_amd.uuu_conv_forward(x, y, w, None, ops.graph_tables(graph), 6, False,
+    c, _ = torch.ops.lunatp.uuu_conv_forward.default(x, y, w, None, ops.graph_tables(graph), 6, False,
                                                  prepared.torch_config)
     assert torch.equal(a, b) and torch.equal(a, c)
 
