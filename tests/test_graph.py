@@ -1,79 +1,77 @@
-"""Graph construction, ordering and ownership (``tests/lunatp/test_make_graph.py:9-55``)."""
+"""Graph tables of ``make_graph`` (``src/lunatp/graph.py:17-141``), CPU builder.
+
+The expected tables live in ``tests/golden/graph_cases.json`` (the reference's
+graph-test vectors plus cases of this build); each case lists only the tables
+it pins.  Derived views name what they check: ``sources_in_src_order`` is
+``src[edge_ids_by_src]``, ``*_degrees_in_*_order`` are row lengths read in a
+launch order.
+"""
+
+import json
+from pathlib import Path
 
 import pytest
 import torch
 
 from lunaequivariance_amd import make_graph
 
-
-def test_destination_sorted_endpoints_are_preserved():
-    src = torch.tensor([2, 0, 1])
-    dst = torch.tensor([0, 1, 2])
-    graph = make_graph(src, dst, 4)
-    assert torch.equal(graph.dst, dst.to(graph.dst.dtype))
-    assert torch.equal(graph.src, src.to(graph.src.dtype))
-    assert graph.dst_rowptr.tolist() == [0, 1, 2, 3, 3]
+CASES = json.loads((Path(__file__).parent / "golden" / "graph_cases.json").read_text())
 
 
-def test_invalid_graph_includes_values():
-    with pytest.raises(ValueError, match="num_nodes=2.*at least 4"):
-        make_graph(torch.tensor([3]), torch.tensor([0]), 2)
-    with pytest.raises(ValueError, match="nonnegative"):
-        make_graph(torch.tensor([-1]), torch.tensor([0]), 2)
-    with pytest.raises(ValueError, match="sorted"):
-        make_graph(torch.tensor([0, 1]), torch.tensor([1, 0]), 2)
-    with pytest.raises(TypeError):
-        make_graph(torch.tensor([0.0]), torch.tensor([0.0]), 1)
-    with pytest.raises(ValueError, match="equal shape"):
-        make_graph(torch.tensor([0, 1]), torch.tensor([0]), 2)
+def _views(graph):
+    ids = graph.edge_ids_by_src.long()
+    return {
+        "num_nodes": lambda: graph.num_nodes,
+        "src": lambda: graph.src.tolist(),
+        "dst": lambda: graph.dst.tolist(),
+        "dst_rowptr": lambda: graph.dst_rowptr.tolist(),
+        "src_rowptr": lambda: graph.src_rowptr.tolist(),
+        "edge_ids_by_src": lambda: graph.edge_ids_by_src.tolist(),
+        "edge_ids_by_dst": lambda: graph.edge_ids_by_dst.tolist(),
+        "sources_in_src_order": lambda: graph.src[ids].tolist(),
+        "dst_degrees_in_node_order": lambda: graph.dst_rowptr.diff()[graph.node_order.long()].tolist(),
+        "src_degrees_in_source_node_order":
+            lambda: graph.src_rowptr.diff()[graph.source_node_order.long()].tolist(),
+        "node_tiers": lambda: graph.node_tiers.tolist(),
+        "segment_nodes": lambda: graph.source_segments.nodes.tolist(),
+    }
 
 
-def test_source_edge_order_is_generated():
-    src = torch.tensor([2, 0, 1, 0])
-    dst = torch.tensor([0, 1, 1, 2])
-    graph = make_graph(src, dst, 3)
-    assert graph.dst.tolist() == [0, 1, 1, 2]
-    assert graph.src[graph.edge_ids_by_src.long()].tolist() == [0, 0, 1, 2]
-    assert graph.src_rowptr.tolist() == [0, 2, 3, 4]
+@pytest.mark.parametrize("case", CASES["cases"], ids=lambda c: c["name"])
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_expected_tables(case, dtype):
+    src = torch.tensor(case["src"], dtype=dtype)
+    dst = torch.tensor(case["dst"], dtype=dtype)
+    graph = make_graph(src, dst, case["num_nodes"])
+    views = _views(graph)
+    for table, expected in case["expect"].items():
+        assert views[table]() == expected, table
+    # Whatever a case pins, the orders are permutations and edge ids cover every edge.
+    assert sorted(graph.edge_ids_by_src.tolist()) == list(range(src.shape[0]))
+    assert sorted(graph.node_order.tolist()) == list(range(graph.num_nodes))
+    assert sorted(graph.source_node_order.tolist()) == list(range(graph.num_nodes))
+
+
+@pytest.mark.parametrize("bad", CASES["errors"], ids=lambda b: f"{b['error']}:{b['match'] or 'dtype'}")
+def test_rejected_inputs(bad):
+    src = torch.tensor(bad["src"])
+    dst = torch.tensor(bad["dst"])
+    error = {"ValueError": ValueError, "TypeError": TypeError}[bad["error"]]
+    with pytest.raises(error, match=bad["match"] or None):
+        make_graph(src, dst, bad["num_nodes"])
 
 
 @pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
-def test_generated_graph_tables_and_input_ownership(dtype):
-    src = torch.tensor([2, 0, 1, 0], dtype=dtype)
-    dst = torch.tensor([0, 1, 1, 2], dtype=dtype)
+def test_graph_owns_copies_of_its_inputs(dtype):
+    src = torch.tensor([3, 1, 0, 2, 2], dtype=dtype)
+    dst = torch.tensor([0, 0, 1, 3, 3], dtype=dtype)
     graph = make_graph(src, dst, 4)
-    assert graph.src_rowptr.tolist() == [0, 2, 3, 4, 4]
-    assert graph.dst_rowptr.tolist() == [0, 1, 3, 4, 4]
-    assert graph.edge_ids_by_src.sort().values.tolist() == [0, 1, 2, 3]
-    assert graph.src[graph.edge_ids_by_src.long()].tolist() == [0, 0, 1, 2]
-    assert graph.edge_ids_by_dst.tolist() == [0, 1, 2, 3]
-    for rowptr, order in ((graph.dst_rowptr, graph.node_order), (graph.src_rowptr, graph.source_node_order)):
-        assert order.sort().values.tolist() == [0, 1, 2, 3]
-        assert rowptr.diff()[order.long()].tolist() == [2, 1, 1, 0]
-    assert graph.src.data_ptr() != src.data_ptr()
-    assert graph.dst.data_ptr() != dst.data_ptr()
-    src.zero_()
-    dst.zero_()
-    assert graph.src.tolist() == [2, 0, 1, 0]
-    assert graph.dst.tolist() == [0, 1, 1, 2]
-
-
-def test_stable_source_permutation_and_column_shapes():
-    """Equal sources keep destination order; [E, 1] inputs are accepted."""
-    src = torch.tensor([[1], [0], [1], [1], [0]])
-    dst = torch.tensor([[0], [0], [1], [2], [2]])
-    graph = make_graph(src, dst)
-    assert graph.num_nodes == 3
-    assert graph.edge_ids_by_src.tolist() == [1, 4, 0, 2, 3]
-
-
-def test_empty_graph_and_segments():
-    empty = torch.zeros(0, dtype=torch.int64)
-    graph = make_graph(empty, empty, 5)
-    assert graph.dst_rowptr.tolist() == [0] * 6
-    assert graph.node_tiers.tolist() == [5, 5, 5]
-    assert graph.source_segments.nodes.tolist() == [0, 1, 2, 3, 4]
-    assert make_graph(empty, empty).num_nodes == 0
+    kept_src, kept_dst = graph.src.tolist(), graph.dst.tolist()
+    assert graph.src.data_ptr() != src.data_ptr() and graph.dst.data_ptr() != dst.data_ptr()
+    src.fill_(1)
+    dst.fill_(2)
+    assert graph.src.tolist() == kept_src == [3, 1, 0, 2, 2]
+    assert graph.dst.tolist() == kept_dst == [0, 0, 1, 3, 3]
 
 
 def test_source_segments_split_long_rows():
