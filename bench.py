@@ -62,8 +62,13 @@ def parse_args():
                         help="UUU configs: time only the fwd+bwd step (for profiler runs)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="only run a 2 GiB device-to-device copy (HBM counter calibration)")
-    parser.add_argument("--cpu-shard", type=int, default=400,
+    parser.add_argument("--summarize-traffic", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
+                        help="write the HBM traffic summary of two rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs "
+                             "(counter_collection.csv files) of this configuration, then exit")
+    parser.add_argument("--cpu-shard", type=int, default=50,
                         help="CPU baseline runs 1/shard of the destination rows")
+    parser.add_argument("--cpu-repeats", type=int, default=5,
+                        help="CPU baseline: timed repeats after one warm-up (median and IQR reported)")
     return parser.parse_args()
 
 
@@ -75,12 +80,49 @@ def algorithmic_bytes(N, E, in1, in2, out, wnum, real, index=4):
     return {"uvu_fwd_p0": fwd, "uvu_bwd_p0": bwd_main, "uvu_bwd_reduce": Y}
 
 
+def step_algorithmic_bytes(N, E, in1, in2, out, wnum, real, double_backward, index=4):
+    """Compulsory bytes per step and kernel name.
+
+    fwd + first-order bwd: the forward reads x, y, w and writes out; the
+    backward reads x, y, w, g and writes gx (through the gx pass), gy (through
+    the partial reduction) and gw.  With the force-training double backward
+    (d gy / d(x, w) along ry, rx = rw = 0) the one extra backward launch reads
+    x, ry, w, g and writes hx and hw.
+    """
+    X, Y, W, O = N * in1 * real, E * in2 * real, E * wnum * real, N * out * real
+    per = algorithmic_bytes(N, E, in1, in2, out, wnum, real, index)
+    launches = {"uvu_fwd_p0": 1, "uvu_bwd_p0": 1, "uvu_bwd_reduce": 1}
+    if double_backward:
+        per["uvu_bwd_p0"] += (X + Y + W + O) + (X + W) + 2 * E * index + (N + 1) * index
+        launches["uvu_bwd_p0"] = 2
+    return per, launches
+
+
+def conv_flops(instructions, in1, in2, out, channels, E):
+    """Arithmetic of one forward over E edges: per edge and channel, 3 flops per
+    Clebsch-Gordan term (x*y, times c, accumulate) plus 2 per output component
+    (times w, accumulate).  The first-order backward does the same work twice
+    (gx and gy/gw contractions of q = C g)."""
+    from oracle.wigner import wigner_3j
+    import numpy as np
+
+    total = 0
+    for i1, i2, io, *_ in instructions:
+        l1, l2, l3 = in1[i1][1].l, in2[i2][1].l, out[io][1].l
+        terms = int(np.count_nonzero(np.abs(wigner_3j(l1, l2, l3)) > 1e-12))
+        total += 3 * terms + 2 * (2 * l3 + 1)
+    return float(total) * channels * E
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the operator would shard by destination-node ranges)", file=sys.stderr)
         sys.exit(2)
+    if args.summarize_traffic:
+        summarize_traffic(args.config, *args.summarize_traffic)
+        return
     import torch
 
     if args.calibrate_copy:
@@ -151,16 +193,18 @@ def main():
     ms_per_step = elapsed * 1000.0 / args.steps
     value = E / (ms_per_step / 1000.0)
 
-    algo = algorithmic_bytes(N, E, conv.irreps_in1.dim, conv.irreps_in2.dim, conv.irreps_out.dim,
-                             conv.weight_numel, real)
+    per_step, launches = step_algorithmic_bytes(N, E, conv.irreps_in1.dim, conv.irreps_in2.dim,
+                                                conv.irreps_out.dim, conv.weight_numel, real,
+                                                cfg["double_backward"])
     per_kernel = {}
     for name, (count, total_ms, low, high) in kernels.items():
         avg = total_ms / count
         entry = {"launches": count, "avg_ms": round(avg, 4), "min_ms": round(low, 4),
                  "max_ms": round(high, 4)}
-        if name in algo and not cfg["double_backward"]:
-            entry["algorithmic_bytes"] = algo[name]
-            entry["gbs"] = round(algo[name] / (avg / 1000.0) / 1e9, 1)
+        if name in per_step:
+            # Average launch: the step's algorithmic bytes of this kernel over its launches.
+            entry["algorithmic_bytes"] = per_step[name] / launches[name]
+            entry["gbs"] = round(per_step[name] / (total_ms / args.steps / 1000.0) / 1e9, 1)
         per_kernel[name] = entry
     dominant = max(kernels, key=lambda n: kernels[n][1]) if kernels else None
     roofline = None
@@ -169,13 +213,21 @@ def main():
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(args.config, dtype, dominant),
-                    "algorithmic_bytes": algo[dominant]}
-    step_bytes = algo["uvu_fwd_p0"] + algo["uvu_bwd_p0"] + algo["uvu_bwd_reduce"]
+                    "algorithmic_bytes": per_kernel[dominant]["algorithmic_bytes"]}
+    step_bytes = sum(per_step.values())
+    step_seconds = ms_per_step / 1000.0
+    extra = {}
+    if dtype == torch.float64:
+        # FP64 roofline next to the HBM one: forward + first-order backward arithmetic.
+        flops = 3.0 * conv_flops(instructions, conv.irreps_in1, conv.irreps_in2, conv.irreps_out,
+                                 cfg["channels"], E)
+        extra["step_fp64_tflops"] = round(flops / step_seconds / 1e12, 2)
+        extra["step_fp64_frac"] = round(flops / step_seconds / 1e12 / FP64_PEAK_TFLOPS, 4)
 
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, args.cpu_shard,
-                           dtype)
+                           dtype, repeats=args.cpu_repeats, double_backward=cfg["double_backward"])
 
     line = {
         "metric": "UVU TP-conv edges/s fwd+bwd",
@@ -197,8 +249,8 @@ def main():
                    "weight_numel": conv.weight_numel, "parallelism": "single GPU"},
         "graph_build_ms": round(statistics.median(graph_ms), 3),
         "step_algorithmic_gb": round(step_bytes / 1e9, 3),
-        "step_hbm_frac": round(step_bytes / (ms_per_step / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)
-        if not cfg["double_backward"] else None,
+        "step_hbm_frac": round(step_bytes / step_seconds / 1e9 / HBM_PEAK_GBS, 4),
+        **extra,
         "roofline": roofline,
         "kernels": per_kernel,
         "cpu_baseline": cpu,
@@ -259,7 +311,7 @@ def bench_uvw(args):
     dominant = max(("uvw_fwd", "uvw_bwd_xy", "uvw_bwd_w"), key=lambda n: kernels[n][1])
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_uvw(ir, sh, instructions, x, y, w, g)
+        cpu = cpu_baseline_uvw(ir, sh, instructions, x, y, w, g, repeats=args.cpu_repeats)
     achieved = per_kernel[dominant]["tflops"]
     print(json.dumps({
         "metric": "UVW shared-weight TP rows/s fwd+bwd", "value": round(rows / (ms / 1000), 1), "unit": "rows/s",
@@ -380,7 +432,8 @@ def bench_uuu(args):
     cpu = None
     if not args.no_cpu_baseline:
         wcpu = w if mode == "uuu" else w.detach().reshape(1, -1).expand(E, -1)
-        cpu = cpu_baseline(ir, edge_ir, ir, instructions, x, y, wcpu, g, src, dst, N, 40, dtype)
+        cpu = cpu_baseline(ir, edge_ir, ir, instructions, x, y, wcpu, g, src, dst, N, 40, dtype,
+                           repeats=args.cpu_repeats)
         # in the metric's unit: the sample's edges/s times the graph's atoms per edge
         cpu["value"] = round(cpu["value"] * N / E, 1)
         cpu["unit"] = "atoms/s"
@@ -408,33 +461,56 @@ def bench_uuu(args):
     }))
 
 
-def cpu_baseline_uvw(ir, sh, instructions, x, y, w, g, sample=20000):
+def cpu_baseline_uvw(ir, sh, instructions, x, y, w, g, sample=20000, repeats=5):
     """The oracle's torch restatement of the UVW product, fp32, fwd+bwd, on the
     first ``sample`` rows, timed on this host's cores."""
     import torch
 
     from oracle.uvw import uvw_tensor_product
 
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     xs = x.detach()[:sample].cpu().clone().requires_grad_()
     ys = y.detach()[:sample].cpu().clone().requires_grad_()
     ws = w.detach().cpu().clone().requires_grad_()
     gs = g[:sample].cpu()
     times = []
-    for repeat in range(4):
+    for repeat in range(repeats + 1):
         start = time.perf_counter()
         out = uvw_tensor_product(ir, sh, ir, instructions, xs, ys, ws)
         torch.autograd.grad(out, (xs, ys, ws), gs)
         times.append(time.perf_counter() - start)
-    timed = times[1:]
-    return {"value": round(sample / statistics.median(timed), 1), "unit": "rows/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"first {sample} of {x.shape[0]} rows, fwd+bwd, median of {len(timed)} after 1 warm-up, "
-                      f"float32"}
+    median, q1, q3 = timing_summary(times[1:])
+    return {"value": round(sample / median, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+            "iqr": [round(sample / q3, 1), round(sample / q1, 1)],
+            "sample": f"first {sample} of {x.shape[0]} rows, fwd+bwd, median of {repeats} after 1 warm-up, "
+                      f"float32, {threads} threads"}
+
+
+KERNEL_SOURCES = {
+    "uvu": ("uvu_emit.cpp", "uvu_schedule.cpp", "uvu_plan.h"),
+    "uuu": ("uuu.cpp",),
+}
+
+
+def kernel_source_digest(config):
+    """SHA-256 of the kernel sources a configuration's kernels are emitted from."""
+    import hashlib
+
+    family = "uuu" if config.startswith("uuu") else "uvu"
+    digest = hashlib.sha256()
+    for name in KERNEL_SOURCES[family]:
+        digest.update((ROOT / "lunaequivariance_amd" / "csrc" / name).read_bytes())
+    return digest.hexdigest()
 
 
 def measured_traffic(config, dtype, kernel):
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter
-    summary (FETCH_SIZE x2 and WRITE_SIZE x1 per the copy calibration), or None."""
+    summary (FETCH_SIZE x2 and WRITE_SIZE x1 per the copy calibration), or None.
+
+    The summary records the digest of the kernel sources it was measured on; a
+    summary of other sources is stale and gives None rather than an old figure.
+    """
     import torch
 
     name = f"hbm_traffic_{config}_{'fp32' if dtype == torch.float32 else 'fp64'}.json"
@@ -442,10 +518,41 @@ def measured_traffic(config, dtype, kernel):
     if not path.exists():
         return None
     data = json.loads(path.read_text())
+    if data.get("source_sha256") != kernel_source_digest(config):
+        return None
     entry = data["kernels"].get(kernel)
     if entry is None:
         return None
     return round((entry["fetch_kib"] * data["fetch_scale"] + entry["write_kib"] * data["write_scale"]) * 1024)
+
+
+# FETCH_SIZE counts half of the bytes a plain 2 GiB device copy reads, WRITE_SIZE
+# all of the bytes it writes (bench.py --calibrate-copy under the same counters).
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+
+
+def summarize_traffic(config, fetch_csv, write_csv, out_json):
+    """Mean FETCH_SIZE / WRITE_SIZE (KiB) per dispatch of every kernel of two
+    rocprofv3 counter runs, with the copy-calibration scales and the digest of the
+    kernel sources measured."""
+    import csv
+    from collections import defaultdict
+
+    kernels = defaultdict(dict)
+    for path, counter, key in ((fetch_csv, "FETCH_SIZE", "fetch_kib"), (write_csv, "WRITE_SIZE", "write_kib")):
+        values = defaultdict(list)
+        with open(path) as handle:
+            for row in csv.DictReader(handle):
+                name = row["Kernel_Name"].split("(")[0]
+                if row["Counter_Name"] == counter and name.startswith("luna_"):
+                    values[name[len("luna_"):]].append(float(row["Counter_Value"]))
+        for name, vals in values.items():
+            kernels[name][key] = round(sum(vals) / len(vals), 2)
+            kernels[name]["dispatches"] = len(vals)
+    summary = {"workload": config, "fetch_scale": FETCH_SCALE, "write_scale": WRITE_SCALE,
+               "per": "mean KiB per dispatch", "source_sha256": kernel_source_digest(config),
+               "kernels": {k: v for k, v in sorted(kernels.items()) if "fetch_kib" in v and "write_kib" in v}}
+    Path(out_json).write_text(json.dumps(summary, indent=1) + "\n")
 
 
 def calibrate_copy():
@@ -466,13 +573,34 @@ def calibrate_copy():
     print(json.dumps({"copy_bytes_per_launch": 2 * n * 4, "copy_gbs": round(2 * n * 4 / seconds / 1e9, 1)}))
 
 
-def cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, shard, dtype):
-    """The oracle's fp32 torch restatement, fwd+bwd, on the edges of the first N/shard
-    destination rows (contiguous in the dst-sorted edge list)."""
+def cpu_threads():
+    """Host threads for the CPU baseline: the job's CPU share (OMP_NUM_THREADS when the
+    launcher sets it), else every core this process may run on."""
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        return int(share)
+    return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+
+
+def timing_summary(times):
+    """Median and interquartile range of repeated timings (seconds)."""
+    ordered = sorted(times)
+    q = statistics.quantiles(ordered, n=4, method="inclusive") if len(ordered) > 1 else [ordered[0]] * 3
+    return statistics.median(ordered), q[0], q[2]
+
+
+def cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, shard, dtype, repeats=5,
+                 double_backward=False):
+    """The oracle's torch restatement, in the workload's dtype, on the edges of the first
+    N/shard destination rows (contiguous in the dst-sorted edge list): the same step as
+    the GPU's (fwd + bwd, plus the gy double backward for the force-training config),
+    timed on this host's cores, median and IQR of ``repeats`` runs after one warm-up."""
     import torch
 
     from oracle.uvu_conv import uvu_conv
 
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     rows = max(1, N // shard)
     dst_cpu = dst.cpu()
     count = int((dst_cpu < rows).sum())
@@ -481,18 +609,27 @@ def cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, sha
     ws = w.detach()[:count].cpu().clone().requires_grad_()
     gs = g[:rows].cpu()
     srcs, dsts = src[:count].cpu(), dst_cpu[:count]
-    threads = torch.get_num_threads()
-    times = []
-    for repeat in range(4):
-        start = time.perf_counter()
+    rys = torch.randn_like(ys)
+
+    def step():
         out = uvu_conv(in1, sh, out_irreps, instructions, xs, ys, ws, srcs, dsts, rows)
-        torch.autograd.grad(out, (xs, ys, ws), gs)
+        grads = torch.autograd.grad(out, (xs, ys, ws), gs, create_graph=double_backward)
+        if double_backward:
+            torch.autograd.grad(grads[1], (xs, ws), rys)
+
+    times = []
+    for repeat in range(repeats + 1):
+        start = time.perf_counter()
+        step()
         times.append(time.perf_counter() - start)
-    timed = times[1:]
-    return {"value": round(count / statistics.median(timed), 1), "unit": "edges/s", "cores": threads,
+    median, q1, q3 = timing_summary(times[1:])
+    return {"value": round(count / median, 1), "unit": "edges/s", "cores": threads,
             "kind": "port",
+            "iqr": [round(count / q3, 1), round(count / q1, 1)],
             "sample": f"{count} edges into the first {rows} of {N} destination rows (1/{shard}), "
-                      f"fwd+bwd, median of {len(timed)} after 1 warm-up, {str(dtype).split('.')[-1]}"}
+                      f"{'fwd+bwd+double-bwd' if double_backward else 'fwd+bwd'}, median of {repeats} after "
+                      f"1 warm-up (iqr = edges/s at the 3rd and 1st quartile times), "
+                      f"{str(dtype).split('.')[-1]}, {threads} threads"}
 
 
 if __name__ == "__main__":

@@ -56,23 +56,42 @@ def parse_irreps(text: str):
 
 
 def path_weights(in1, in2, out, instructions, irrep_normalization="component",
-                 path_normalization="element"):
-    """sqrt(alpha) per instruction (``layout.py:323-370``), unit variances."""
+                 path_normalization="element", in1_var=None, in2_var=None, out_var=None):
+    """sqrt(alpha) per instruction (``layout.py:323-370``).
+
+    alpha = a_irrep / x * out_var[io] * user_weight, with a_irrep = 2 l3 + 1
+    ("component"), (2 l1 + 1)(2 l2 + 1) ("norm") or 1 ("none"), and x = the sum
+    over the instructions into the same output of in1_var * in2_var * fan
+    ("element"), this instruction's in1_var * in2_var * fan times the number of
+    instructions into its output ("path"), or 1 ("none"); fan = mul2 (uvu),
+    mul1 * mul2 (uvw), 1 (uuu).  Variances default to 1 per irrep block.
+    """
+    v1 = [1.0] * len(in1) if in1_var is None else [float(v) for v in in1_var]
+    v2 = [1.0] * len(in2) if in2_var is None else [float(v) for v in in2_var]
+    vo = [1.0] * len(out) if out_var is None else [float(v) for v in out_var]
+    if (len(v1), len(v2), len(vo)) != (len(in1), len(in2), len(out)):
+        raise ValueError("one variance per irrep block is required")
+
+    def fan(ins):
+        mode = ins[3]
+        return v1[ins[0]] * v2[ins[1]] * {"uvu": in2[ins[1]][0], "uvw": in1[ins[0]][0] * in2[ins[1]][0],
+                                          "uuu": 1}[mode]
+
     weights = []
-    for i1, i2, io, mode, _has_w, *rest in instructions:
+    for ins in instructions:
+        i1, i2, io, mode, _has_w, *rest = ins
         user = rest[0] if rest else 1.0
         l1, l2, l3 = in1[i1][1], in2[i2][1], out[io][1]
         alpha = {"component": 2 * l3 + 1, "norm": (2 * l1 + 1) * (2 * l2 + 1), "none": 1}[irrep_normalization]
-        fan = lambda ins: {"uvu": in2[ins[1]][0], "uvw": in1[ins[0]][0] * in2[ins[1]][0], "uuu": 1}[ins[3]]
         if path_normalization == "element":
             x = sum(fan(other) for other in instructions if other[2] == io)
         elif path_normalization == "path":
-            x = fan((i1, i2, io, mode)) * sum(1 for other in instructions if other[2] == io)
+            x = fan(ins) * sum(1 for other in instructions if other[2] == io)
         else:
             x = 1
         if x > 0:
             alpha /= x
-        weights.append(math.sqrt(alpha * user))
+        weights.append(math.sqrt(alpha * vo[io] * user))
     return weights
 
 
@@ -125,13 +144,15 @@ def edge_messages(in1, in2, out, instructions, x_src, y, w, weights=None):
 
 
 def conv(irreps_in1, irreps_in2, irreps_out, instructions, x, y, w, src, dst, num_nodes,
-             env=None, return_l0=False):
+             env=None, return_l0=False, normalization=None):
     """Reference semantics of ``TensorProductConv(...)(x, y, w, graph=..., env=, return_l0_feat=)``
-    for uvu or uuu instructions."""
+    for uvu or uuu instructions.  ``normalization``: keyword arguments of
+    ``path_weights`` (irrep/path normalisation and variances); defaults otherwise."""
     in1, in2, out = parse_irreps(irreps_in1), parse_irreps(irreps_in2), parse_irreps(irreps_out)
     src = torch.as_tensor(src).long()
     dst = torch.as_tensor(dst).long()
-    msg, pieces = edge_messages(in1, in2, out, instructions, x[src], y, w)
+    weights = path_weights(in1, in2, out, instructions, **(normalization or {}))
+    msg, pieces = edge_messages(in1, in2, out, instructions, x[src], y, w, weights)
     scaled = msg if env is None else msg * env.reshape(-1, 1)
     result = x.new_zeros((num_nodes, msg.shape[1])).index_add(0, dst, scaled)
     if not return_l0:

@@ -150,3 +150,79 @@ def test_golden_fixtures(name):
     second = torch.autograd.grad(first, leaves, (t["rx"], t["ry"], t["rw"]))
     for a, k in zip(second, ("hx", "hy", "hw")):
         assert torch.allclose(a, t[k], atol=1e-12)
+
+
+# Closed forms of layout.py:323-370 with non-unit variances, written out by hand.
+# Two uvu paths 0e x 0e -> 0e and 1o x 1o -> 0e, edge multiplicity 2, variances
+# in1 = (2, 3), in2 = (5, 7), out = (11):
+#   element: x = 2*5*2 + 3*7*2 = 62 for both paths;
+#   path:    x = 2*5*2*2 = 40 and 3*7*2*2 = 84 (two paths into the output);
+#   none:    x = 1.
+# The "norm" irrep normalisation multiplies by d1*d2 = 1 and 9 instead of d3 = 1.
+VAR_CASE = dict(in1="3x0e+3x1o", in2="2x0e+2x1o", out="3x0e",
+                instructions=[(0, 0, 0, "uvu", True), (1, 1, 0, "uvu", True)],
+                variances=dict(in1_var=[2.0, 3.0], in2_var=[5.0, 7.0], out_var=[11.0]))
+VAR_EXPECTED = {
+    ("component", "element"): [math.sqrt(11 / 62), math.sqrt(11 / 62)],
+    ("component", "path"): [math.sqrt(11 / 40), math.sqrt(11 / 84)],
+    ("component", "none"): [math.sqrt(11), math.sqrt(11)],
+    ("norm", "element"): [math.sqrt(11 / 62), math.sqrt(9 * 11 / 62)],
+    ("norm", "path"): [math.sqrt(11 / 40), math.sqrt(9 * 11 / 84)],
+    ("none", "none"): [math.sqrt(11), math.sqrt(11)],
+}
+
+
+@pytest.mark.parametrize("irrep_norm,path_norm", sorted(VAR_EXPECTED))
+def test_path_weights_with_variances_closed_form(irrep_norm, path_norm):
+    c = VAR_CASE
+    weights = path_weights(parse_irreps(c["in1"]), parse_irreps(c["in2"]), parse_irreps(c["out"]),
+                           c["instructions"], irrep_normalization=irrep_norm, path_normalization=path_norm,
+                           **c["variances"])
+    assert weights == pytest.approx(VAR_EXPECTED[irrep_norm, path_norm], rel=1e-15)
+
+
+def test_path_weights_user_weight_and_component_dimension():
+    """1o x 0e -> 1o and 1o x 1e -> 1o into 3x1o, edge multiplicity 2, in1 var 2, in2 vars
+    (5, 7), out var 4, user path weights 0.5 and 1: element x = 2*5*2 + 2*7*2 = 48, so
+    alpha = 3 * 4 / 48 times the user weight."""
+    instructions = [(0, 0, 0, "uvu", True, 0.5), (0, 1, 0, "uvu", True, 1.0)]
+    weights = path_weights(parse_irreps("3x1o"), parse_irreps("2x0e+2x1e"), parse_irreps("3x1o"), instructions,
+                           in1_var=[2.0], in2_var=[5.0, 7.0], out_var=[4.0])
+    assert weights == pytest.approx([math.sqrt(0.5 * 12 / 48), math.sqrt(12 / 48)], rel=1e-15)
+
+
+def test_path_weights_reject_wrong_variance_lengths():
+    with pytest.raises(ValueError):
+        path_weights(parse_irreps("3x0e"), parse_irreps("1x0e"), parse_irreps("3x0e"), [(0, 0, 0, "uvu", True)],
+                     in1_var=[1.0, 2.0])
+
+
+@pytest.mark.parametrize("irrep_norm,path_norm", sorted(VAR_EXPECTED))
+def test_package_normalisation_with_variances_matches_pinned_oracle(irrep_norm, path_norm):
+    from lunaequivariance_amd import TensorProductConfig
+
+    c = VAR_CASE
+    tp = TensorProductConfig(c["in1"], c["in2"], c["out"], c["instructions"], internal_weights=False,
+                             shared_weights=False, irrep_normalization=irrep_norm, path_normalization=path_norm,
+                             **c["variances"])
+    assert [i.path_weight for i in tp.instructions] == pytest.approx(VAR_EXPECTED[irrep_norm, path_norm],
+                                                                     rel=1e-14)
+
+
+def test_conv_uses_normalisation_arguments():
+    """Doubling out_var scales the convolution by sqrt(2); "none"/"none" equals the
+    unnormalised brute force times sqrt(out_var)."""
+    c = VAR_CASE
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(4, 12, generator=gen, dtype=torch.float64)
+    y = torch.randn(6, 8, generator=gen, dtype=torch.float64)
+    w = torch.randn(6, 12, generator=gen, dtype=torch.float64)
+    src, dst = torch.tensor([0, 1, 3, 2, 2, 0]), torch.tensor([0, 0, 1, 2, 3, 3])
+    args = (c["in1"], c["in2"], c["out"], c["instructions"], x, y, w, src, dst, 4)
+    base = uvu_conv(*args, normalization=dict(c["variances"]))
+    doubled = uvu_conv(*args, normalization=dict(c["variances"], out_var=[22.0]))
+    assert torch.allclose(doubled, base * math.sqrt(2), rtol=1e-13, atol=0)
+    plain = uvu_conv(*args, normalization=dict(irrep_normalization="none", path_normalization="none"))
+    brute = brute_force(*args)
+    # brute_force uses the default (component, element) weights: both paths sqrt(1 / (2 + 2)).
+    assert torch.allclose(plain * 0.5, torch.as_tensor(brute), rtol=1e-12, atol=1e-13)

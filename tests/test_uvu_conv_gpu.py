@@ -48,11 +48,12 @@ def inputs(conv, nodes, edges, dtype, gen):
 
 
 def check_orders(conv, in1, in2, out, instructions, x, y, w, src, dst, nodes, dtype, gen,
-                 env=None, l0=False, orders=3):
+                 env=None, l0=False, orders=3, normalization=None):
     """Forward and derivatives up to ``orders`` against the oracle's autograd."""
     ref_args = [t.clone().requires_grad_() for t in (x, y, w)]
     ref_env = None if env is None else env.clone().requires_grad_()
-    ref = uvu_conv(in1, in2, out, instructions, *ref_args, src, dst, nodes, env=ref_env, return_l0=l0)
+    ref = uvu_conv(in1, in2, out, instructions, *ref_args, src, dst, nodes, env=ref_env, return_l0=l0,
+                   normalization=normalization)
     ref = ref if isinstance(ref, tuple) else (ref,)
     dev_args = [t.to(DEV, dtype).requires_grad_() for t in (x, y, w)]
     dev_env = None if env is None else env.to(DEV, dtype).requires_grad_()
@@ -379,3 +380,98 @@ def test_graph_capture_replays():
         expected = (eo, *torch.autograd.grad(eo, (ex, ey, ew), ng))
         for n, (a, b) in enumerate(zip(static, expected)):
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-6), f"replay {replay}, output {n}"
+
+
+@pytest.mark.parametrize("irrep_norm,path_norm", [("norm", "path"), ("component", "none"), ("none", "element")])
+def test_nondefault_normalisation_and_variances(irrep_norm, path_norm):
+    """Path weights from non-default normalisation and non-unit variances
+    (src/lunatp/utils/layout.py:323-370) reach the kernels: parity to second order."""
+    in1, sh, out = "8x0e+8x1o+8x2e", "2x0e+2x1o", "8x0e+8x1o+8x2e+8x1e"
+    instructions = all_uvu_instructions(in1, sh, out)
+    variances = dict(in1_var=[0.5, 2.0, 3.0], in2_var=[1.5, 0.25], out_var=[2.0, 0.5, 4.0, 1.25])
+    norm = dict(irrep_normalization=irrep_norm, path_normalization=path_norm)
+    conv = lunaeq.TensorProductConv(in1, sh, out, instructions, internal_weights=False, shared_weights=False,
+                                    dtype=torch.float32, **norm, **variances)
+    gen = torch.Generator().manual_seed(21)
+    nodes, edges = 9, 40
+    src, dst = random_graph(nodes, edges, gen)
+    x, y, w = inputs(conv, nodes, edges, torch.float32, gen)
+    check_orders(conv, in1, sh, out, instructions, x, y, w, src, dst, nodes, torch.float32, gen, orders=2,
+                 normalization=dict(norm, **variances))
+
+
+def test_cfg4_layout_force_training_small():
+    """Config 4's layer (64 channels, lmax 3, every uvu path, fp32): forward, first order
+    and the force-training double backward d<ry, gy>/d(x, w) against the oracle."""
+    from lunaequivariance_amd.workloads import mace_irreps
+
+    in1, sh, out, instructions = mace_irreps(64, 3)
+    conv = make_conv(in1, sh, out, instructions, torch.float32)
+    gen = torch.Generator().manual_seed(44)
+    nodes, edges = 11, 70
+    src, dst = random_graph(nodes, edges, gen)
+    x, y, w = inputs(conv, nodes, edges, torch.float32, gen)
+    g = torch.randn(nodes, conv.irreps_out.dim, generator=gen, dtype=torch.float64)
+    ry = torch.randn(edges, conv.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ref = uvu_conv(in1, sh, out, instructions, *ref_in, src, dst, nodes)
+    rgx, rgy, rgw = torch.autograd.grad(ref, ref_in, g, create_graph=True)
+    rhx, rhw = torch.autograd.grad(rgy, (ref_in[0], ref_in[2]), ry)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    graph = conv.create_graph(src.to(DEV), dst.to(DEV), nodes)
+    act = conv(*dev_in, graph=graph)
+    gx, gy, gw = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32), create_graph=True)
+    hx, hw = torch.autograd.grad(gy, (dev_in[0], dev_in[2]), ry.to(DEV, torch.float32))
+    for a, r, name in ((act, ref, "out"), (gx, rgx, "gx"), (gy, rgy, "gy"), (gw, rgw, "gw"),
+                       (hx, rhx, "hx"), (hw, rhw, "hw")):
+        assert_close(a, r, torch.float32, name)
+
+
+def test_cfg4_full_size_sampled_rows():
+    """Config 4 at full size (10,000 atoms, ~520k edges, 64 channels, fp32): the bench's
+    force-training step, checked on sampled destination rows (out, gy, gw, hw) and
+    source rows (gx, hx) against the oracle evaluated on just those rows."""
+    from lunaequivariance_amd.workloads import mace_irreps, periodic_radius_graph, spherical_harmonics
+
+    dtype = torch.float32
+    in1, sh, out, instructions = mace_irreps(64, 3)
+    conv = make_conv(in1, sh, out, instructions, dtype)
+    N = 10000
+    src, dst, _, vec, _ = periodic_radius_graph(N, 0.1, 5.0, seed=0, device=DEV)
+    E = src.numel()
+    assert 500_000 < E < 545_000
+    graph = conv.create_graph(src, dst, N)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    x = torch.randn(N, conv.irreps_in1.dim, device=DEV, dtype=dtype, generator=gen).requires_grad_()
+    y = spherical_harmonics(3, vec).to(dtype).requires_grad_()
+    w = (torch.randn(E, conv.weight_numel, device=DEV, dtype=dtype, generator=gen) / 34 ** 0.5).requires_grad_()
+    g = torch.randn(N, conv.irreps_out.dim, device=DEV, dtype=dtype, generator=gen)
+    ry = torch.randn(E, conv.irreps_in2.dim, device=DEV, dtype=dtype, generator=gen)
+    result = conv(x, y, w, graph=graph)
+    gx, gy, gw = torch.autograd.grad(result, (x, y, w), g, create_graph=True)
+    hx, hw = torch.autograd.grad(gy, (x, w), ry)
+    pick = torch.randperm(N, generator=torch.Generator().manual_seed(2))[:8]
+    src_c, dst_c = src.cpu(), dst.cpu()
+    x64, y64, w64, g64, ry64 = (t.detach().double().cpu() for t in (x, y, w, g, ry))
+    for node in pick.tolist():
+        edges = torch.nonzero(dst_c == node).flatten()
+        local_dst = torch.zeros(len(edges), dtype=torch.long)
+        leaves = [x64.clone().requires_grad_(), y64[edges].clone().requires_grad_(),
+                  w64[edges].clone().requires_grad_()]
+        ref = uvu_conv(in1, sh, out, instructions, *leaves, src_c[edges], local_dst, 1)
+        assert_close(result[node:node + 1], ref, dtype, f"out[{node}]")
+        rgx, rgy, rgw = torch.autograd.grad(ref, leaves, g64[node:node + 1], create_graph=True)
+        assert_close(gy[edges.to(DEV)], rgy, dtype, f"gy of edges into {node}")
+        assert_close(gw[edges.to(DEV)], rgw, dtype, f"gw of edges into {node}")
+        (rhw,) = torch.autograd.grad(rgy, leaves[2], ry64[edges])
+        assert_close(hw[edges.to(DEV)], rhw, dtype, f"hw of edges into {node}")
+    for node in pick[:4].tolist():
+        edges = torch.nonzero(src_c == node).flatten()
+        targets, local_dst = torch.unique(dst_c[edges], return_inverse=True)
+        xs = x64.clone().requires_grad_()
+        ys = y64[edges].clone().requires_grad_()
+        ref = uvu_conv(in1, sh, out, instructions, xs, ys, w64[edges], src_c[edges], local_dst, len(targets))
+        rgx, rgy = torch.autograd.grad(ref, (xs, ys), g64[targets], create_graph=True)
+        assert_close(gx[node:node + 1], rgx[node:node + 1], dtype, f"gx[{node}]")
+        (rhx,) = torch.autograd.grad(rgy, xs, ry64[edges])
+        assert_close(hx[node:node + 1], rhx[node:node + 1], dtype, f"hx[{node}]")
