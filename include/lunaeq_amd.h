@@ -135,6 +135,29 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* plan,
                       void* workspace, size_t workspace_bytes,
                       int64_t num_nodes, int64_t num_edges, LunaStream stream);
 
+/*
+ * Allocation-free first-order backward: luna_uvu_conv_bwd with its workspace
+ * taken from a static device array of LUNA_UVU_NOALLOC_SCRATCH_BYTES (64 MiB)
+ * that every GPU the library runs on holds until the process ends.  It calls no
+ * hipMalloc/hipFree; problems whose workspace (luna_uvu_conv_bwd_workspace)
+ * exceeds the array are refused with an error.  The first call on a device
+ * looks up the array's device address (and, like every entry point, loads the
+ * plan's kernels on first use); make one call before capturing a HIP graph.
+ * All calls on one GPU share its array: calls that overlap on one GPU race.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid it).
+ */
+#define LUNA_UVU_NOALLOC_SCRATCH_BYTES (64ull << 20)
+size_t luna_uvu_conv_bwd_noalloc_limit(void);
+int luna_uvu_conv_bwd_noalloc(const LunaUvuPlan* plan,
+                              const void* x, const void* y, const void* w, const void* env,
+                              const void* g, const void* gl0,
+                              const int32_t* src, const int32_t* dst_rowptr,
+                              const int32_t* node_order,
+                              const int32_t* src_rowptr, const int32_t* edge_ids_by_src,
+                              void* gx, void* gy, void* gw, void* genv,
+                              int64_t num_nodes, int64_t num_edges, LunaStream stream);
+
 /* ------------------------------------------------------------------------ */
 /* Shared-weight UVW tensor product (fp32, matrix cores).                    */
 

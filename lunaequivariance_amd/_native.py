@@ -37,6 +37,8 @@ PROTOTYPES = {
     "luna_uvu_conv_bwd_workspace": (ctypes.c_int, [_VP, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_uvu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 5 + [_VP] * 5
                           + [ctypes.c_size_t, _I64, _I64, _VP]),
+    "luna_uvu_conv_bwd_noalloc_limit": (ctypes.c_size_t, []),
+    "luna_uvu_conv_bwd_noalloc": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 5 + [_VP] * 4 + [_I64, _I64, _VP]),
     "luna_uvw_plan_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_VP)]),
     "luna_uvw_plan_destroy": (ctypes.c_int, [_VP]),
     "luna_uvw_plan_needs_zero": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_int32)]),

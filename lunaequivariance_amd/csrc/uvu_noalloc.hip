@@ -1,0 +1,75 @@
+// Allocation-free variant of the UVU first-order backward.
+//
+// luna_uvu_conv_bwd takes a caller-allocated workspace (the gy partial sums
+// and the per-edge gx messages).  Callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops) use
+// luna_uvu_conv_bwd_noalloc instead: its workspace is `scratch`, a file-scope
+// device array of LUNA_UVU_NOALLOC_SCRATCH_BYTES that every GPU the library
+// runs on holds until the process ends.  Problems needing more are refused.
+//
+// `scratch` is a device symbol: on the host its name is only a stand-in, so
+// host code never passes it to a kernel.  The device address is looked up once
+// per device with hipGetSymbolAddress (with that device current) and only that
+// address is used.  Every call on one GPU shares its array and leaves the last
+// call's contents there: calls that overlap on one GPU (other streams, other
+// threads) race.  The kernels write every partial they read, and the gx
+// messages are zero-filled by a kernel when the plan needs it, so nothing
+// has to start at zero.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/lunaeq_amd.h"
+#include "uvu_plan.h"
+
+namespace {
+
+__device__ __align__(256) unsigned char scratch[LUNA_UVU_NOALLOC_SCRATCH_BYTES];
+
+std::mutex scratch_mutex;
+std::vector<void*> scratch_by_device;
+
+// Device address of `scratch` on the current device (looked up on first use).
+void* scratch_address() {
+  int device = -1;
+  luna::check_hip(hipGetDevice(&device), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if ((int)scratch_by_device.size() <= device) scratch_by_device.resize(device + 1, nullptr);
+  if (!scratch_by_device[device]) {
+    void* address = nullptr;
+    luna::check_hip(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!address) luna::fail("hipGetSymbolAddress(scratch) returned a null address");
+    scratch_by_device[device] = address;
+  }
+  return scratch_by_device[device];
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t luna_uvu_conv_bwd_noalloc_limit(void) { return LUNA_UVU_NOALLOC_SCRATCH_BYTES; }
+
+int luna_uvu_conv_bwd_noalloc(const LunaUvuPlan* cplan, const void* x, const void* y, const void* w,
+                              const void* env, const void* g, const void* gl0, const int32_t* src,
+                              const int32_t* dst_rowptr, const int32_t* node_order, const int32_t* src_rowptr,
+                              const int32_t* edge_ids_by_src, void* gx, void* gy, void* gw, void* genv,
+                              int64_t num_nodes, int64_t num_edges, LunaStream stream) {
+  return luna::guard_call([&] {
+    if (!cplan) luna::fail("luna_uvu_conv_bwd_noalloc: null plan");
+    if (num_nodes < 0 || num_edges < 0) luna::fail("luna_uvu_conv_bwd_noalloc: negative problem size");
+    luna::Plan& plan = const_cast<LunaUvuPlan*>(cplan)->plan;
+    const size_t need = luna::uvu_bwd_workspace_bytes(plan, num_edges);
+    if (need > LUNA_UVU_NOALLOC_SCRATCH_BYTES)
+      luna::fail("luna_uvu_conv_bwd_noalloc: " + std::to_string(num_edges) + " edges need " +
+                 std::to_string(need) + " bytes of workspace, above the static scratch of " +
+                 std::to_string((unsigned long long)LUNA_UVU_NOALLOC_SCRATCH_BYTES) +
+                 " bytes; use luna_uvu_conv_bwd with a caller workspace");
+    luna::uvu_conv_bwd(plan, x, y, w, env, g, gl0, src, dst_rowptr, node_order, src_rowptr, edge_ids_by_src,
+                       gx, gy, gw, genv, scratch_address(), LUNA_UVU_NOALLOC_SCRATCH_BYTES, num_nodes, num_edges,
+                       stream);
+  });
+}
+
+}  // extern "C"

@@ -93,5 +93,19 @@ void build_schedule(Plan& plan);
 std::string emit_forward(const Plan& plan, bool env, bool l0);
 std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bool want_msg, bool want_part);
 
+// The first-order backward launches (luna_uvu_conv_bwd without the plan
+// check), with the caller's workspace of uvu_bwd_workspace_bytes bytes.
+size_t uvu_bwd_workspace_bytes(const Plan& plan, int64_t num_edges);
+void uvu_conv_bwd(Plan& plan, const void* x, const void* y, const void* w, const void* env, const void* g,
+                  const void* gl0, const int32_t* src, const int32_t* dst_rowptr, const int32_t* node_order,
+                  const int32_t* src_rowptr, const int32_t* edge_ids_by_src, void* gx, void* gy, void* gw,
+                  void* genv, void* workspace, size_t workspace_bytes, int64_t num_nodes, int64_t num_edges,
+                  void* stream);
+
 
 }  // namespace luna
+
+// The C-ABI's opaque plan handle (include/lunaeq_amd.h).
+struct LunaUvuPlan {
+  luna::Plan plan;
+};

@@ -8,10 +8,6 @@
 
 using namespace luna;
 
-struct LunaUvuPlan {
-  Plan plan;
-};
-
 namespace {
 
 std::string source_for(const Plan& plan, const std::string& variant) {
@@ -49,6 +45,70 @@ void check_sizes(int64_t num_nodes, int64_t num_edges) {
 }
 
 }  // namespace
+
+namespace luna {
+
+// Size of the backward workspace (gy partials, then gx messages).
+size_t uvu_bwd_workspace_bytes(const Plan& plan, int64_t num_edges) {
+  return part_bytes(plan, num_edges) + msg_bytes(plan, num_edges);
+}
+
+void uvu_conv_bwd(Plan& plan, const void* x, const void* y, const void* w, const void* env, const void* g,
+                  const void* gl0, const int32_t* src, const int32_t* dst_rowptr, const int32_t* node_order,
+                  const int32_t* src_rowptr, const int32_t* edge_ids_by_src, void* gx, void* gy, void* gw,
+                  void* genv, void* workspace, size_t workspace_bytes, int64_t num_nodes, int64_t num_edges,
+                  LunaStream stream) {
+  check_sizes(num_nodes, num_edges);
+    if (num_nodes == 0) return;
+    if (!x || !g || !dst_rowptr || !node_order || !src_rowptr) fail("luna_uvu_conv_bwd: null tensor");
+    if (num_edges > 0 && (!y || !w || !src || !edge_ids_by_src)) fail("luna_uvu_conv_bwd: null edge tensor");
+    if (gl0 && plan.spec.l0_dim == 0) gl0 = nullptr;
+    if (!env) genv = nullptr;
+    if (gw && plan.spec.w_broadcast) fail("luna_uvu_conv_bwd: a broadcast weight row has no per-edge gradient");
+    int64_t E = num_edges;
+    const bool want_parts = (gy || genv) && E > 0;
+    const bool want_msg = gx && E > 0;
+    const size_t pbytes = part_bytes(plan, E), mbytes = msg_bytes(plan, E);
+    if ((want_parts || want_msg) && (!workspace || workspace_bytes < pbytes + mbytes))
+      fail("luna_uvu_conv_bwd: workspace too small");
+    void* part = want_parts ? workspace : nullptr;
+    void* msg = want_msg ? (void*)((char*)workspace + pbytes) : nullptr;
+    std::string variant = std::string("bwd") + (env ? '1' : '0') + (gl0 ? '1' : '0') + (gw ? '1' : '0') +
+                          (want_msg ? '1' : '0') + (want_parts ? '1' : '0');
+    hipModule_t module = module_for(plan, variant);
+    hipStream_t s = (hipStream_t)stream;
+    if (want_msg && plan.bwd_gx_needs_zero) {
+      int64_t n = E * (int64_t)plan.spec.in1;
+      void* args[] = {&msg, &n};
+      launch("uvu_fill", function_for(module, "luna_uvu_fill"), dim3((unsigned)((n + 255) / 256)), dim3(256), s,
+             args);
+    }
+    if (E > 0 && (gw || want_parts || want_msg)) {
+      for (int phase = 0; phase < plan.bwd_phases; ++phase) {
+        hipFunction_t f = function_for(module, "luna_uvu_bwd_p" + std::to_string(phase));
+        void* args[] = {&x, &y, &w, &env, &g, &gl0, &src, &dst_rowptr, &node_order, &gw, &msg, &part, &E};
+        launch("uvu_bwd_p" + std::to_string(phase), f,
+               grid_for(num_nodes, plan.bwd_phase_slots[phase], plan.bwd_block_waves[phase]),
+               dim3(64 * std::max(plan.bwd_block_waves[phase], 1)), s, args);
+      }
+    }
+    if (want_parts) {
+      void* args[] = {&part, &gy, &genv, &E};
+      launch("uvu_bwd_reduce", function_for(module, "luna_uvu_bwd_reduce"), dim3((unsigned)((E + 255) / 256)),
+             dim3(256), s, args);
+    }
+    if (gx) {
+      // With no edges the gather still writes zeros (every source row is empty).
+      void* args[] = {&msg, &src_rowptr, &edge_ids_by_src, &gx};
+      const int vec = gather_vector_width(plan);
+      const int64_t per_block = 256LL * vec;
+      launch("uvu_bwd_gather", function_for(module, "luna_uvu_bwd_gather"),
+             dim3((unsigned)num_nodes, (unsigned)((plan.spec.in1 + per_block - 1) / per_block)), dim3(256), s,
+             args);
+    }
+}
+
+}  // namespace luna
 
 extern "C" {
 
@@ -123,7 +183,7 @@ int luna_uvu_conv_bwd_workspace(const LunaUvuPlan* plan, int64_t num_nodes, int6
   return guard_call([&] {
     if (!plan || !bytes) fail("luna_uvu_conv_bwd_workspace: null argument");
     if (num_nodes < 0 || num_edges < 0) fail("negative problem size");
-    *bytes = part_bytes(plan->plan, num_edges) + msg_bytes(plan->plan, num_edges);
+    *bytes = uvu_bwd_workspace_bytes(plan->plan, num_edges);
   });
 }
 
@@ -135,55 +195,9 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* cplan, const void* x, const void* y, co
                       LunaStream stream) {
   return guard_call([&] {
     if (!cplan) fail("luna_uvu_conv_bwd: null plan");
-    Plan& plan = const_cast<LunaUvuPlan*>(cplan)->plan;
-    check_sizes(num_nodes, num_edges);
-    if (num_nodes == 0) return;
-    if (!x || !g || !dst_rowptr || !node_order || !src_rowptr) fail("luna_uvu_conv_bwd: null tensor");
-    if (num_edges > 0 && (!y || !w || !src || !edge_ids_by_src)) fail("luna_uvu_conv_bwd: null edge tensor");
-    if (gl0 && plan.spec.l0_dim == 0) gl0 = nullptr;
-    if (!env) genv = nullptr;
-    if (gw && plan.spec.w_broadcast) fail("luna_uvu_conv_bwd: a broadcast weight row has no per-edge gradient");
-    int64_t E = num_edges;
-    const bool want_parts = (gy || genv) && E > 0;
-    const bool want_msg = gx && E > 0;
-    const size_t pbytes = part_bytes(plan, E), mbytes = msg_bytes(plan, E);
-    if ((want_parts || want_msg) && (!workspace || workspace_bytes < pbytes + mbytes))
-      fail("luna_uvu_conv_bwd: workspace too small");
-    void* part = want_parts ? workspace : nullptr;
-    void* msg = want_msg ? (void*)((char*)workspace + pbytes) : nullptr;
-    std::string variant = std::string("bwd") + (env ? '1' : '0') + (gl0 ? '1' : '0') + (gw ? '1' : '0') +
-                          (want_msg ? '1' : '0') + (want_parts ? '1' : '0');
-    hipModule_t module = module_for(plan, variant);
-    hipStream_t s = (hipStream_t)stream;
-    if (want_msg && plan.bwd_gx_needs_zero) {
-      int64_t n = E * (int64_t)plan.spec.in1;
-      void* args[] = {&msg, &n};
-      launch("uvu_fill", function_for(module, "luna_uvu_fill"), dim3((unsigned)((n + 255) / 256)), dim3(256), s,
-             args);
-    }
-    if (E > 0 && (gw || want_parts || want_msg)) {
-      for (int phase = 0; phase < plan.bwd_phases; ++phase) {
-        hipFunction_t f = function_for(module, "luna_uvu_bwd_p" + std::to_string(phase));
-        void* args[] = {&x, &y, &w, &env, &g, &gl0, &src, &dst_rowptr, &node_order, &gw, &msg, &part, &E};
-        launch("uvu_bwd_p" + std::to_string(phase), f,
-               grid_for(num_nodes, plan.bwd_phase_slots[phase], plan.bwd_block_waves[phase]),
-               dim3(64 * std::max(plan.bwd_block_waves[phase], 1)), s, args);
-      }
-    }
-    if (want_parts) {
-      void* args[] = {&part, &gy, &genv, &E};
-      launch("uvu_bwd_reduce", function_for(module, "luna_uvu_bwd_reduce"), dim3((unsigned)((E + 255) / 256)),
-             dim3(256), s, args);
-    }
-    if (gx) {
-      // With no edges the gather still writes zeros (every source row is empty).
-      void* args[] = {&msg, &src_rowptr, &edge_ids_by_src, &gx};
-      const int vec = gather_vector_width(plan);
-      const int64_t per_block = 256LL * vec;
-      launch("uvu_bwd_gather", function_for(module, "luna_uvu_bwd_gather"),
-             dim3((unsigned)num_nodes, (unsigned)((plan.spec.in1 + per_block - 1) / per_block)), dim3(256), s,
-             args);
-    }
+    uvu_conv_bwd(const_cast<LunaUvuPlan*>(cplan)->plan, x, y, w, env, g, gl0, src, dst_rowptr, node_order,
+                 src_rowptr, edge_ids_by_src, gx, gy, gw, genv, workspace, workspace_bytes, num_nodes, num_edges,
+                 stream);
   });
 }
 
