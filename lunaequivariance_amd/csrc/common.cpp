@@ -59,6 +59,11 @@ void check_hip(hipError_t status, const char* what) {
 std::vector<char> compile_hip(const std::string& source, const std::string& cache_dir, const std::string& tag) {
   std::string key_text = source;
   for (int n = 0; n < kNumOptions; ++n) key_text += kOptions[n];
+  // The compiler's version is part of the key: a code object built by another
+  // hipRTC is never reused (the target architecture is in kOptions).
+  int major = 0, minor = 0;
+  if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) major = minor = -1;
+  key_text += "hiprtc-" + std::to_string(major) + "." + std::to_string(minor);
   key_text += "luna-1";
   char key[32];
   std::snprintf(key, sizeof(key), "%016llx", (unsigned long long)fnv1a(key_text));

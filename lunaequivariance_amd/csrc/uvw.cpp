@@ -1006,11 +1006,37 @@ int bw_pieces(const UvwSpec& s, int floats_per_row) { return (s.wrows * floats_p
 int bw_lds_bytes(const UvwSpec& s, const UvwPath& q) {
   return 4 * 2 * (bw_pieces(s, q.mul1 * q.d1) * 4 + bw_pieces(s, q.mul3 * q.d3) * 4 + 64) * 4;
 }
-bool bw_dma_path(const UvwSpec& s, const UvwPath& q) {
+bool bw_dma_eligible(const UvwSpec& s, const UvwPath& q) {
   if (!s.wdma) return false;
   return q.mul2 == 1 && (q.mul1 * q.d1) % 4 == 0 && (q.mul3 * q.d3) % 4 == 0 && q.x_off % 4 == 0 &&
          q.out_off % 4 == 0 && s.in1 % 4 == 0 && s.out % 4 == 0 && q.d2 * s.wrows <= 64 &&
          bw_lds_bytes(s, q) <= 128 * 1024;
+}
+// The paths that use the LDS copies.  They share one buffer sized by the
+// largest x block and the largest seed block over the set, which may come
+// from different paths: the widest paths leave the set until that union fits
+// the 128 KiB budget.
+std::vector<bool> bw_dma_set(const UvwSpec& s) {
+  std::vector<bool> in(s.paths.size());
+  for (size_t p = 0; p < s.paths.size(); ++p) in[p] = bw_dma_eligible(s, s.paths[p]);
+  for (;;) {
+    int xmax = 0, gmax = 0, widest = -1, width = -1;
+    for (size_t p = 0; p < s.paths.size(); ++p) {
+      if (!in[p]) continue;
+      const UvwPath& q = s.paths[p];
+      const int x = bw_pieces(s, q.mul1 * q.d1) * 4, g = bw_pieces(s, q.mul3 * q.d3) * 4;
+      xmax = std::max(xmax, x);
+      gmax = std::max(gmax, g);
+      if (x + g > width) width = x + g, widest = (int)p;
+    }
+    if (widest < 0 || 4 * 2 * (xmax + gmax + 64) * 4 <= 128 * 1024) return in;
+    in[widest] = false;
+  }
+}
+bool bw_dma_path(const UvwSpec& s, const UvwPath& q) {
+  const size_t p = (size_t)(&q - s.paths.data());
+  if (p >= s.paths.size()) return false;
+  return bw_dma_set(s)[p];
 }
 
 // All such paths in one function (four __restrict__ buffers, so the

@@ -23,6 +23,9 @@ DEV = "cuda"
     ("32x0e+32x1o", "1x0e+1x1o", "48x0e+50x1o+8x2e", 70),                   # LDS-copied, 64-wide and narrow units
     ("64x0e+32x1o", "2x0e+1x1o", "64x0e+64x1o", 50),                        # mul2 = 2 with 32-w seed chunks
     ("16x0e+16x1o", "1x0e+1x1o", "64x0e+64x1o+16x2e", 45),                  # two LDS-copied chunks per path
+    ("64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e", "64x0e+64x1o+64x2e", 600),     # config 5 layer, 3 weight chunks
+    ("256x0e+256x2e", "1x0e+1x1o+1x2e", "256x0e+256x2e", 300),              # LDS-copy union over paths
+    ("192x0e+192x3o", "1x0e+1x3o", "192x0e+192x3o", 260),                   # wide degree-3 blocks
 ])
 def test_uvw_forward_and_two_orders(in1, in2, out, rows):
     instructions = uvw_instructions(in1, in2, out)
