@@ -544,7 +544,7 @@ def summarize_traffic(config, fetch_csv, write_csv, out_json):
         with open(path) as handle:
             for row in csv.DictReader(handle):
                 name = row["Kernel_Name"].split("(")[0]
-                if row["Counter_Name"] == counter and name.startswith("luna_"):
+                if row["Counter_Name"] == counter and name.startswith("luna_") and "graph_" not in name:
                     values[name[len("luna_"):]].append(float(row["Counter_Value"]))
         for name, vals in values.items():
             kernels[name][key] = round(sum(vals) / len(vals), 2)
