@@ -73,13 +73,25 @@ def graph_tables(graph) -> list:
     return [getattr(graph, name) for name in GRAPH_TABLES] + seg + [graph.node_tiers]
 
 
+def _index32(table, bound):
+    """int32 view of a graph table; 64-bit tables (the reference's wide-offset
+    graphs) are narrowed, which is exact while node and edge counts are below
+    2^31 (the kernels compute element offsets in 64 bits either way)."""
+    if table.dtype == torch.int32:
+        return table
+    if bound >= (1 << 31) - 1:
+        raise OverflowError("graph node or edge count exceeds signed int32 capacity")
+    return table.to(torch.int32)
+
+
 def _tables(tables, num_nodes) -> GraphTables:
     if len(tables) != NUM_TABLES:
         raise ValueError(f"expected {NUM_TABLES} graph tables, got {len(tables)}")
     for name, table in zip(GRAPH_TABLES, tables):
         if table is None:
             raise ValueError(f"graph table {name!r} is required")
-    return GraphTables(*tables[:len(GRAPH_TABLES)], num_nodes=int(num_nodes))
+    bound = max(int(num_nodes), int(tables[0].numel()))
+    return GraphTables(*(_index32(t, bound) for t in tables[:len(GRAPH_TABLES)]), num_nodes=int(num_nodes))
 
 
 # ---------------------------------------------------------------------------

@@ -154,8 +154,10 @@ class LunaTPUUUConv:
     def __init__(self, meta, *, dtype=torch.float32, index_bits=32):
         if dtype not in (torch.float32, torch.float64):
             raise ValueError("UUU convolution requires float32 or float64.")
-        if index_bits != 32:
-            raise ValueError("only 32-bit graph indexing is supported")
+        # Element offsets are 64-bit in every kernel, so both index widths run the
+        # same kernels; graph tables are int32 (counts below 2^31).
+        if index_bits not in (32, 64):
+            raise ValueError(f"index_bits must be 32 or 64, got {index_bits}")
         specs = list(meta["generated_specs"])
         if any(int(s["channels"]) < 0 for s in specs):
             raise ValueError("UUU convolution requires nonnegative channels for every path.")

@@ -92,8 +92,10 @@ class LunaTPUVWConv:
         dtype = getattr(paths, "dtype", torch.float32) if dtype is None else dtype
         if dtype not in (torch.float32, torch.float64):
             raise ValueError(f"UVW convolution requires float32 or float64, got {dtype}")
-        if index_bits != 32:
-            raise ValueError("only 32-bit graph indexing is supported")
+        # Element offsets are 64-bit in every kernel, so both index widths run the
+        # same kernels; graph tables are int32 (counts below 2^31).
+        if index_bits not in (32, 64):
+            raise ValueError(f"index_bits must be 32 or 64, got {index_bits}")
         self.tp = paths
         self.compute_dtype = dtype
         self.index_bits = index_bits

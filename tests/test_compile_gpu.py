@@ -255,3 +255,25 @@ def test_double_backward_op_skips_absent_cotangents():
         assert (a is None) == (b is None)
         if a is not None:
             assert_close(a, b.double(), torch.float32, "zero vs marker")
+
+
+def test_wide_index_config_with_int64_tables_matches():
+    """A 64-bit-indexing config with the reference's int64 tables gives the same result as the
+    32-bit path (the kernels use 64-bit element offsets either way)."""
+    import json as _json
+
+    conv, graph, x, y, w = problem(seed=17)
+    data = _json.loads(conv.op.torch_config)
+    data["index_bits"] = 64
+    wide_config = _json.dumps(data, separators=(",", ":"))
+    tables = ops.graph_tables(graph)
+    tables64 = [None if t is None else t.to(torch.int64) for t in tables]
+    a, _ = torch.ops.lunatp.uvu_conv_forward.default(x, y, w, None, tables, graph.num_nodes, False,
+                                                     conv.op.torch_config)
+    b, _ = torch.ops.lunatp.uvu_conv_forward.default(x, y, w, None, tables64, graph.num_nodes, False, wide_config)
+    assert torch.equal(a, b)
+    g = torch.randn_like(a)
+    ga = torch.autograd.grad(a, (x, y, w), g)
+    gb = torch.autograd.grad(b, (x, y, w), g)
+    for p, q in zip(ga, gb):
+        assert torch.equal(p, q)

@@ -121,3 +121,24 @@ def test_fake_kernels_give_reference_shapes(env_shape):
         triple = torch.ops.lunatp.uvu_conv_triple_backward.default(
             x, y, w, env, g, gl0, x, y, w, env, x, y, w, g, env, gl0, tables, N, [True] * 10, config)
         assert len(triple) == 10 and triple[6].shape == x.shape and triple[4].shape == g.shape
+
+
+def test_wide_index_configs_and_int64_tables():
+    """The reference's 64-bit indexing mode (src/lunatp/utils/layout.py:441-517): a config with
+    index_bits=64 restores to an operator, and int64 graph tables (get_graph_with_int64_offsets)
+    are narrowed while counts fit int32 (element offsets are 64-bit in every kernel)."""
+    conv = conv_of()
+    data = json.loads(conv.op.torch_config)
+    data["index_bits"] = 64
+    wide = ops.restore_operator(json.dumps(data, separators=(",", ":")))
+    assert wide.index_bits == 64 and wide.meta == conv.op.meta
+    src = torch.tensor([1, 2, 0, 3, 3, 1])
+    dst = torch.tensor([0, 0, 1, 1, 2, 3])
+    graph = conv.create_graph(src, dst, 4)
+    tables64 = [None if t is None else t.to(torch.int64) for t in ops.graph_tables(graph)]
+    narrowed = ops._tables(tables64, 4)
+    assert narrowed.src.dtype == torch.int32 and torch.equal(narrowed.dst_rowptr, graph.dst_rowptr)
+    with pytest.raises(OverflowError):
+        ops._tables(tables64, 1 << 31)
+    with pytest.raises(ValueError):
+        ops.restore_operator(json.dumps(dict(data, index_bits=16), separators=(",", ":")))
