@@ -604,9 +604,25 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     int shift = 0, low = 0;
     std::string total = emit_butterfly(c, values, tag.c_str(), &shift, &low);
     c.line("        const int col = lane >> %d;", shift);
-    c.line("        if ((lane & %d) == 0 && col < %zu)", low, values.size());
-    c.line("          part[((i64)(%d + (slot - %d)) * E + e) * PART_W + %d + col] = %s;", g.gy_slot_base,
-           g.slot_base, column[values[0]], total.c_str());
+    c.line("        const bool own = (lane & %d) == 0 && col < %zu;", low, values.size());
+    if (g.pair_partials) {
+      // Chunk 1 hands its sums to chunk 0 (two buffers by edge parity: one
+      // barrier per edge orders both uses).
+      c.line("        const int par = (e - beg) & 1;");
+      c.line("        if (slot - %d == 1) {", g.slot_base);
+      c.line("          if (own) gy_share[par][%d + col] = %s;", column[values[0]], total.c_str());
+      c.line("          __syncthreads();");
+      c.line("        } else {");
+      c.line("          __syncthreads();");
+      c.line("          if (own)");
+      c.line("            part[((i64)%d * E + e) * PART_W + %d + col] = %s + gy_share[par][%d + col];",
+             g.gy_slot_base, column[values[0]], total.c_str(), column[values[0]]);
+      c.line("        }");
+    } else {
+      c.line("        if (own)");
+      c.line("          part[((i64)(%d + (slot - %d)) * E + e) * PART_W + %d + col] = %s;", g.gy_slot_base,
+             g.slot_base, column[values[0]], total.c_str());
+    }
     c.line("      }");
   };
   for (int n = 0; n < np; ++n) {
@@ -859,6 +875,9 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     for (const Group& g : plan.bwd_groups)
       if (g.phase == phase && g.subsets > 1) share_d1 = std::max(share_d1, g.d1);
     if (share_d1 > 0 && want_msg) c.line("  __shared__ real msg_share[2][%d][64];", share_d1);
+    bool pairs = false;
+    for (const Group& g : plan.bwd_groups) pairs = pairs || (g.phase == phase && g.pair_partials);
+    if (pairs && want_part) c.line("  __shared__ real gy_share[2][PART_W];");
     if (waves == 0) {
       // One wave per workgroup, the slots of a node on consecutive workgroups.
       c.line("  const int lane = threadIdx.x;");
@@ -893,6 +912,7 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     for (int sub = 0; sub < g.subsets; ++sub) {
       GroupUse use = group_use(spec, g.subsets > 1 ? subset_view(g, sub) : g);
       for (int chunk = 0; chunk < g.chunks; ++chunk) {
+        if (g.pair_partials && chunk > 0) continue;  // chunk 1's share is in chunk 0's slot
         const int slot = g.gy_slot_base + chunk * g.subsets + sub;
         int col = 0;
         for (int yi : use.ys) writers[yi].push_back({slot, col++});

@@ -52,6 +52,9 @@ struct Group {
   int slot_base = 0;                 // first grid.y slot of this group in its phase
   bool gx_accumulate = false;        // backward: gx block shared with another group
   int gy_slot_base = 0;              // backward: first partial slot of this group
+  // Backward: the group's two 64-channel chunks run as the two waves of one
+  // workgroup and add their gy partials through LDS into one slot.
+  bool pair_partials = false;
   // Backward: the paths may be split into `subsets` path sets, each run by
   // its own wave (slot = chunk * subsets + subset); the two waves of a split
   // group share a workgroup and sum their gx messages through LDS.

@@ -316,13 +316,10 @@ void build_schedule(Plan& plan) {
   // group starts on an even slot, so its waves pair up in one workgroup), and
   // gy partial slots are global.
   std::vector<int> slots(bwd_phases, 0);
-  int parts = 0;
   for (Group& g : plan.bwd_groups) {
     if (g.subsets > 1 && slots[g.phase] % 2) ++slots[g.phase];
     g.slot_base = slots[g.phase];
     slots[g.phase] += g.chunks * g.subsets;
-    g.gy_slot_base = parts;
-    parts += g.chunks * g.subsets;
   }
   plan.bwd_phases = bwd_phases;
   plan.bwd_phase_slots = slots;
@@ -334,6 +331,17 @@ void build_schedule(Plan& plan) {
   if (const char* e = std::getenv("LUNAEQ_AMD_WG")) limit = std::max(0, std::min(16, std::atoi(e)));
   for (int s : plan.phase_slots) plan.fwd_block_waves.push_back(std::min(s, limit));
   for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(any_split ? 2 : std::min(s, limit));
+  // A group whose two chunks are the two waves of one workgroup adds their gy
+  // partials through LDS and writes one slot (half the partial traffic).
+  bool pair = true;
+  if (const char* e = std::getenv("LUNAEQ_AMD_PAIRGY")) pair = std::atoi(e) != 0;
+  int parts = 0;
+  for (Group& g : plan.bwd_groups) {
+    g.pair_partials = pair && g.subsets == 1 && g.chunks == 2 && g.slot_base % 2 == 0 &&
+                      plan.bwd_block_waves[g.phase] == 2;
+    g.gy_slot_base = parts;
+    parts += g.pair_partials ? 1 : g.chunks * g.subsets;
+  }
   plan.gy_parts = parts;
   for (int s : slots)
     if (s > 65535) fail("too many channel chunks for one launch");
