@@ -174,6 +174,32 @@ void launch(const std::string& name, hipFunction_t f, dim3 grid, dim3 block, hip
   }
 }
 
+hipStream_t side_stream() {
+  static std::mutex lock;
+  static std::vector<hipStream_t> streams;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  std::lock_guard<std::mutex> guard(lock);
+  if ((int)streams.size() <= device) streams.resize(device + 1, nullptr);
+  if (!streams[device]) check_hip(hipStreamCreateWithFlags(&streams[device], hipStreamNonBlocking), "hipStreamCreate");
+  return streams[device];
+}
+
+void fork_join(hipStream_t stream, const std::function<void(hipStream_t)>& side, const std::function<void()>& main) {
+  hipStream_t other = side_stream();
+  hipEvent_t fork = nullptr, join = nullptr;
+  check_hip(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "hipEventCreate");
+  check_hip(hipEventCreateWithFlags(&join, hipEventDisableTiming), "hipEventCreate");
+  check_hip(hipEventRecord(fork, stream), "hipEventRecord");
+  check_hip(hipStreamWaitEvent(other, fork, 0), "hipStreamWaitEvent");
+  side(other);
+  check_hip(hipEventRecord(join, other), "hipEventRecord");
+  main();
+  check_hip(hipStreamWaitEvent(stream, join, 0), "hipStreamWaitEvent");
+  check_hip(hipEventDestroy(fork), "hipEventDestroy");
+  check_hip(hipEventDestroy(join), "hipEventDestroy");
+}
+
 int guard_call(const std::function<void()>& body) {
   try {
     body();

@@ -40,6 +40,16 @@ hipFunction_t function_for(hipModule_t module, const std::string& name);
 void launch(const std::string& name, hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, void** args,
             unsigned shared_bytes = 0);
 
+// A second stream of the current device (created once, default priority,
+// non-blocking), for work that may run beside the caller's stream.
+hipStream_t side_stream();
+
+// Runs `side` on side_stream() and `main` on `stream` concurrently: the side
+// stream starts after everything already queued on `stream`, and `stream`
+// continues only after the side work (events fork and join them, so a HIP
+// graph captured on `stream` records both branches).
+void fork_join(hipStream_t stream, const std::function<void(hipStream_t)>& side, const std::function<void()>& main);
+
 // Runs body(); returns 0, or 1 with the message kept for luna_last_error().
 int guard_call(const std::function<void()>& body);
 

@@ -1335,6 +1335,12 @@ size_t gw_part_bytes(const UvwPlan& p, int64_t rows) {
 size_t gy_part_bytes(const UvwPlan& p, int64_t rows) {
   return align256((size_t)p.gy_slots * (size_t)rows * (size_t)p.spec.in2 * sizeof(float));
 }
+// LUNAEQ_AMD_UVW_CONC=0 runs the two backward kernels one after the other.
+bool concurrent_backward() {
+  const char* e = std::getenv("LUNAEQ_AMD_UVW_CONC");
+  return !e || std::atoi(e) != 0;
+}
+
 unsigned row_blocks(int64_t rows, int rows_per_wave) {  // 4 waves per workgroup
   return (unsigned)((rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave));
 }
@@ -1461,34 +1467,47 @@ int luna_uvw_bwd(const LunaUvwPlan* cplan, const void* x, const void* y, const v
     char* ws = (char*)workspace;
     void* gw_part = ws;
     void* gy_part = ws + gw_part_bytes(plan, rows);
-    if ((gx || gy) && rows > 0) {
-      if (!gx || !gy) fail("luna_uvw_bwd: gx and gy are produced together");
+    if ((gx || gy) && rows > 0 && (!gx || !gy)) fail("luna_uvw_bwd: gx and gy are produced together");
+    // gx/gy and the weight gradient read the same inputs and write disjoint
+    // outputs; each leaves the matrix cores partly idle, so with both wanted
+    // the weight gradient runs on a second stream beside gx/gy.
+    auto run_xy = [&](hipStream_t st) {
       hipModule_t module = module_for(plan, "bxy");
       for (int phase = 0; phase < plan.bwd_phases; ++phase) {
         void* args[] = {&x, &y, &weight, &g, &gx, &gy_part, &B};
         launch("uvw_bwd_xy", function_for(module, "luna_uvw_bwd_xy_p" + std::to_string(phase)),
-               dim3((unsigned)((rows + 15) / 16), (unsigned)plan.bwd_phase_tiles[phase]), dim3(256), s, args);
+               dim3((unsigned)((rows + 15) / 16), (unsigned)plan.bwd_phase_tiles[phase]), dim3(256), st, args);
       }
       void* args[] = {&gy_part, &gy, &B};
       launch("uvw_bwd_gy", function_for(module, "luna_uvw_bwd_gy"), dim3((unsigned)((rows + 255) / 256)), dim3(256),
-             s, args);
-    }
-    if (gw) {
+             st, args);
+    };
+    auto run_w = [&](hipStream_t st) {
       hipModule_t module = module_for(plan, "bw");
       const int64_t chunks = chunks_for(plan, rows);
       if (rows > 0) {
         void* args[] = {&x, &y, &g, &gw_part, &B};
         launch("uvw_bwd_w", function_for(module, "luna_uvw_bwd_w"),
-               dim3((unsigned)((chunks + 3) / 4), (unsigned)plan.spec.paths.size()), dim3(256), s, args);
+               dim3((unsigned)((chunks + 3) / 4), (unsigned)plan.spec.paths.size()), dim3(256), st, args);
       }
       int n = (int)chunks;
       void* part2 = (char*)gw_part + align256((size_t)chunks * (size_t)plan.spec.wnum * sizeof(float));
       void* args[] = {&gw_part, &part2, &n};
       launch("uvw_bwd_w_reduce", function_for(module, "luna_uvw_bwd_w_reduce"),
-             dim3((unsigned)((plan.spec.wnum + 255) / 256), kReduceGroups), dim3(256), s, args);
+             dim3((unsigned)((plan.spec.wnum + 255) / 256), kReduceGroups), dim3(256), st, args);
       void* args2[] = {&part2, &gw};
       launch("uvw_bwd_w_final", function_for(module, "luna_uvw_bwd_w_final"),
-             dim3((unsigned)((plan.spec.wnum + 255) / 256)), dim3(256), s, args2);
+             dim3((unsigned)((plan.spec.wnum + 255) / 256)), dim3(256), st, args2);
+    };
+    const bool want_xy = (gx || gy) && rows > 0;
+    if (want_xy && gw && concurrent_backward()) {
+      // Load both modules first: nothing below may block between fork and join.
+      module_for(plan, "bxy");
+      module_for(plan, "bw");
+      fork_join(s, run_w, [&] { run_xy(s); });
+    } else {
+      if (want_xy) run_xy(s);
+      if (gw) run_w(s);
     }
   });
 }
