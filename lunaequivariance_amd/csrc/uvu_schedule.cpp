@@ -256,10 +256,66 @@ void build_schedule(Plan& plan) {
     for (auto& b : g.blocks) b.accumulate = collision;
   plan.fwd_phases = assign_phases(plan.fwd_groups, out_ranges);
   plan.phase_slots.assign(plan.fwd_phases, 0);
-  for (Group& g : plan.fwd_groups) {
-    g.slot_base = plan.phase_slots[g.phase];
-    plan.phase_slots[g.phase] += g.chunks;
+  // Two waves per workgroup: the two 64-channel chunks of a 128-channel group
+  // gather adjacent halves of the same x rows together.  (All slots of a node
+  // in one workgroup, or the slots of a node on consecutive workgroups, keep
+  // every input block's gathers live at once and measured slower.)
+  int limit = 2;
+  if (const char* e = std::getenv("LUNAEQ_AMD_WG")) limit = std::max(0, std::min(16, std::atoi(e)));
+  bool sibling_pairs = true;
+  if (const char* e = std::getenv("LUNAEQ_AMD_FWDPAIR")) sibling_pairs = std::atoi(e) != 0;
+  for (int phase = 0; phase < plan.fwd_phases; ++phase) {
+    std::vector<Group*> members;
+    for (Group& g : plan.fwd_groups)
+      if (g.phase == phase) members.push_back(&g);
+    auto key = [](const Group* g) { return std::make_tuple(g->x_off, g->d1, g->channels); };
+    // An input block split over several groups (its accumulators exceed the
+    // budget) is gathered by each of them.  Two such sibling groups of two
+    // chunks each run as the four waves of one workgroup, so that their
+    // gathers of the same x rows arrive together and the second is served by
+    // the first's cache lines instead of a second trip to the fabric.
+    bool siblings = false, two_chunks = true;
+    for (size_t a = 0; a < members.size(); ++a) {
+      two_chunks = two_chunks && members[a]->chunks == 2;
+      for (size_t b = a + 1; b < members.size(); ++b) siblings = siblings || key(members[a]) == key(members[b]);
+    }
+    int slot = 0;
+    if (sibling_pairs && siblings && two_chunks && limit == 2) {
+      std::vector<bool> placed(members.size(), false);
+      std::vector<Group*> singles;
+      for (size_t a = 0; a < members.size(); ++a) {
+        if (placed[a]) continue;
+        placed[a] = true;
+        size_t b = a + 1;
+        while (b < members.size() && (placed[b] || key(members[b]) != key(members[a]))) ++b;
+        if (b == members.size()) {
+          singles.push_back(members[a]);
+          continue;
+        }
+        placed[b] = true;
+        members[a]->slot_base = slot;
+        members[b]->slot_base = slot + 2;
+        slot += 4;
+      }
+      for (Group* g : singles) {
+        g->slot_base = slot;
+        slot += 2;
+      }
+      slot += slot % 4;  // the last workgroup's idle half, if any
+      plan.fwd_block_waves.push_back(4);
+    } else {
+      for (Group* g : members) {
+        g->slot_base = slot;
+        slot += g->chunks;
+      }
+      plan.fwd_block_waves.push_back(std::min(slot, limit));
+    }
+    plan.phase_slots[phase] = slot;
   }
+  // The kernels test slots in group order.
+  std::stable_sort(plan.fwd_groups.begin(), plan.fwd_groups.end(), [](const Group& a, const Group& b) {
+    return std::make_pair(a.phase, a.slot_base) < std::make_pair(b.phase, b.slot_base);
+  });
   for (int s : plan.phase_slots)
     if (s > 65535) fail("too many channel chunks for one launch");
 
@@ -323,13 +379,7 @@ void build_schedule(Plan& plan) {
   }
   plan.bwd_phases = bwd_phases;
   plan.bwd_phase_slots = slots;
-  // Two waves per workgroup: the two 64-channel chunks of a 128-channel group
-  // gather adjacent halves of the same x rows together.  (All slots of a node
-  // in one workgroup, or the slots of a node on consecutive workgroups, keep
-  // every input block's gathers live at once and measured slower.)
-  int limit = 2;
-  if (const char* e = std::getenv("LUNAEQ_AMD_WG")) limit = std::max(0, std::min(16, std::atoi(e)));
-  for (int s : plan.phase_slots) plan.fwd_block_waves.push_back(std::min(s, limit));
+  // The backward uses the forward's two waves per workgroup.
   for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(any_split ? 2 : std::min(s, limit));
   // A group whose two chunks are the two waves of one workgroup adds their gy
   // partials through LDS and writes one slot (half the partial traffic).
