@@ -49,7 +49,12 @@ struct UvwSpec {
   int wide = 2;
   bool wdma = true;
   int bcy = -1;  // LUNAEQ_AMD_UVW_BCY: gx/gy contraction as (c y) dZ (1) or c (y dZ) (0); -1: by occupancy
-  int gpad = 4;  // LUNAEQ_AMD_UVW_GPAD: seed-row padding in the gx/gy staging (1: scalar LDS writes)
+  // LUNAEQ_AMD_UVW_GPAD: seed-row padding in the gx/gy staging (1: scalar LDS
+  // writes, 2: pairs, 4: 16-byte writes).  With rows 32 d3 + 2 floats apart,
+  // the B-operand reads of one half-wave (16 rows x two w) fall in 32
+  // distinct banks (0.863 -> 0.822 ms against 32 d3 + 4 at config 5).
+  int gpad = 2;
+  int wpad = 2;  // LUNAEQ_AMD_UVW_WPAD: weight-row padding (2: the A-operand reads conflict-free, as above)
   int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
   int wrows = 2;  // LUNAEQ_AMD_UVW_WROWS: batch rows per LDS copy of the weight gradient (2, or 4)
 };
@@ -761,7 +766,7 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
     // the same 16 batch rows and share the staged seed rows.
     if (stage_d3) {
       c.line("  __shared__ __attribute__((aligned(16))) real gs[2][16][%d];", cw * stage_d3 + s.gpad);
-      c.line("  __shared__ real wsh[4][16][%d];", cw + 1);
+      c.line("  __shared__ real wsh[4][16][%d];", cw + s.wpad);
       c.line("  int chunk = 0;");
     }
     c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
@@ -869,6 +874,9 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
               c.line("            real* dst = &gsb[r][e * 4];");
               if (s.gpad == 4)
                 c.line("            *(float4*)dst = pg%d;", it);
+              else if (s.gpad == 2)
+                c.line("            ((float2*)dst)[0] = make_float2(pg%d.x, pg%d.y); ((float2*)dst)[1] = "
+                       "make_float2(pg%d.z, pg%d.w);", it, it, it, it);
               else
                 c.line("            dst[0] = pg%d.x; dst[1] = pg%d.y; dst[2] = pg%d.z; dst[3] = pg%d.w;", it, it, it, it);
               c.line("          }");
@@ -1363,7 +1371,11 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     p.spec.wdma = !wdma || std::atoi(wdma) != 0;
     if (const char* wr = std::getenv("LUNAEQ_AMD_UVW_WROWS")) p.spec.wrows = std::atoi(wr) == 4 ? 4 : 2;
     if (const char* cy = std::getenv("LUNAEQ_AMD_UVW_BCY")) p.spec.bcy = std::atoi(cy);
-    if (const char* gp = std::getenv("LUNAEQ_AMD_UVW_GPAD")) p.spec.gpad = std::atoi(gp) == 1 ? 1 : 4;
+    if (const char* gp = std::getenv("LUNAEQ_AMD_UVW_GPAD")) {
+      const int v = std::atoi(gp);
+      p.spec.gpad = v == 1 || v == 4 ? v : 2;
+    }
+    if (const char* wp = std::getenv("LUNAEQ_AMD_UVW_WPAD")) p.spec.wpad = std::atoi(wp) == 1 ? 1 : 2;
     if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
