@@ -206,3 +206,44 @@ def test_uvw_random_layouts(in1, in2, out, rows):
     dev_first = torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32))
     for n, (a, r) in enumerate(zip(dev_first, ref_first)):
         assert_close(a, r, torch.float32, f"first-order {n}")
+
+
+def test_uvw_graph_capture_replays():
+    """Forward and backward (whose weight-gradient half runs on a library stream,
+    forked from and joined back to the capturing stream) captured in a HIP graph
+    and replayed with new inputs, each replay against eager."""
+    ir, sh = "64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e"
+    instructions = uvw_instructions(ir, sh, ir)
+    tp = lunaeq.TensorProduct(ir, sh, ir, instructions, shared_weights=True, internal_weights=False)
+    rows = 600
+    gen = torch.Generator().manual_seed(5)
+    shapes = [(rows, tp.irreps_in1.dim), (rows, tp.irreps_in2.dim), (tp.weight_numel,), (rows, tp.irreps_out.dim)]
+    sx, sy, sw, sg = (torch.randn(s, generator=gen).to(DEV) for s in shapes)
+    sx.requires_grad_(), sy.requires_grad_(), sw.requires_grad_()
+
+    def step():
+        o = tp(sx, sy, sw)
+        return (o, *torch.autograd.grad(o, (sx, sy, sw), sg))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    captured = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(captured):
+        static = step()
+    for replay in range(3):
+        new = [torch.randn(s, generator=gen).to(DEV) for s in shapes]
+        with torch.no_grad():
+            for dst, src in zip((sx, sy, sw, sg), new):
+                dst.copy_(src)
+        captured.replay()
+        torch.cuda.synchronize()
+        ex, ey, ew = (t.clone().requires_grad_() for t in new[:3])
+        eo = tp(ex, ey, ew)
+        expected = (eo, *torch.autograd.grad(eo, (ex, ey, ew), new[3]))
+        for n, (a, b) in enumerate(zip(static, expected)):
+            scale = b.abs().max()
+            assert (a - b).abs().max() <= 1e-5 * scale + 1e-6, f"replay {replay}, output {n}"
