@@ -64,6 +64,8 @@ struct Options {
   bool y_vgpr = true;    // copy y into vector registers before use: a scalar
                          // operand makes a VALU op issue at half rate
   bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
+  int hoist_regs = -1;   // registers the backward may spend on q classes computed once
+                         // per node instead of per edge (-1: by precision)
   int fwd_local = 0;     // forward in per-path form (no products shared between
                          // paths): fewer registers, more arithmetic; 1 on, 0 off
                          // (fp64 measured 10.5 -> 10.0 ms with it off)
@@ -96,6 +98,7 @@ Options options() {
   o.fwd_local = value("flocal", o.fwd_local);
   o.bwd_prefetch = value("bpre", o.bwd_prefetch);
   o.hoist = value("hoist", o.hoist) != 0;
+  o.hoist_regs = value("hq", o.hoist_regs);
   o.fwd_wpe = value("fwpe", o.fwd_wpe);
   o.bwd_wpe = value("bwpe", o.bwd_wpe);
   o.out_lds = value("olds", o.out_lds) != 0;
@@ -578,6 +581,83 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
       seeds.push_back("G" + std::to_string(b) + "_" + std::to_string(k));
     }
   }
+  // Some q classes are computed once per node, before the edge loop, within
+  // a register budget: classes of two or more terms first (each saves that
+  // many instructions per edge), then single-term ones, cheapest first (a
+  // seed all of whose classes are hoisted leaves the loop, so hoisting its
+  // only class costs no register).
+  std::vector<std::vector<SignedClass>> path_classes(np);
+  std::map<std::pair<int, size_t>, std::string> hoisted;  // (path, class) -> register name
+  {
+    struct Candidate {
+      int n;
+      size_t cls;
+      int terms;
+      std::vector<std::string> uses;
+    };
+    std::vector<Candidate> cands;
+    std::map<std::string, int> users;  // seed -> classes reading it
+    for (int n = 0; n < np; ++n) {
+      const Path& q = spec.paths[g.paths[n]];
+      std::map<std::pair<int, int>, std::vector<const Term*>> by_ij;
+      for (const Term& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
+      path_classes[n] = signed_classes(by_ij);
+      const bool scalar_seed = gl0 && q.l0_col >= 0;
+      for (size_t m = 0; m < path_classes[n].size(); ++m) {
+        Candidate cd{n, m, (int)path_classes[n][m].coefficients.size(), {}};
+        for (const auto& kc : path_classes[n][m].coefficients)
+          cd.uses.push_back("G" + std::to_string(g.path_block[n]) + "_" + std::to_string(kc.first));
+        for (const auto& u : cd.uses) ++users[u];
+        if (!scalar_seed) cands.push_back(cd);
+      }
+    }
+    const int per_value = bits / 32;
+    int budget = opt.hoist_regs >= 0 ? opt.hoist_regs : (bits == 32 ? 24 : 36);
+    std::map<std::string, int> left = users;  // classes per seed not yet hoisted
+    int extra = 0;                            // registers: hoisted values minus freed seeds
+    auto cost = [&](const Candidate& cd) {
+      int freed = 0;
+      for (const auto& u : cd.uses) freed += left[u] == 1;
+      return per_value * (1 - freed);
+    };
+    auto take = [&](const Candidate& cd) {
+      extra += cost(cd);
+      for (const auto& u : cd.uses) --left[u];
+      hoisted[{cd.n, cd.cls}] = "H" + std::to_string(cd.n) + "_" + std::to_string(cd.cls);
+    };
+    std::stable_sort(cands.begin(), cands.end(), [](const Candidate& a, const Candidate& b) { return a.terms > b.terms; });
+    for (const auto& cd : cands)
+      if (cd.terms > 1 && extra + cost(cd) <= budget) take(cd);
+    for (bool progress = true; progress;) {
+      progress = false;
+      const Candidate* best = nullptr;
+      for (const auto& cd : cands)
+        if (cd.terms == 1 && !hoisted.count({cd.n, cd.cls}) && extra + cost(cd) <= budget &&
+            (!best || cost(cd) < cost(*best)))
+          best = &cd;
+      if (best) {
+        take(*best);
+        progress = true;
+      }
+    }
+    for (const auto& kv : hoisted) {
+      const SignedClass& cls = path_classes[kv.first.first][kv.first.second];
+      const int b = g.path_block[kv.first.first];
+      std::string expr;
+      for (const auto& kc : cls.coefficients) {
+        const std::string seed = "G" + std::to_string(b) + "_" + std::to_string(kc.first);
+        expr = expr.empty() ? literal(kc.second, bits) + " * " + seed
+                            : "FMA(" + literal(kc.second, bits) + ", " + seed + ", " + expr + ")";
+      }
+      c.line("    real %s = %s;", kv.second.c_str(), expr.c_str());
+    }
+    // Seeds still read in the loop, and the hoisted values, stay resident.
+    std::vector<std::string> resident;
+    for (const auto& name : seeds)
+      if (left[name] > 0) resident.push_back(name);
+    for (const auto& kv : hoisted) resident.push_back(kv.second);
+    seeds = resident;
+  }
   auto body = [&]() {
   if (!opt.hoist) {
     // Opaque to the optimiser: keeps the edge-invariant q_ij inside the loop
@@ -633,37 +713,41 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     c.line("        const real wv = w%d;", n);
     if (scalar_seed) c.line("        const real S0 = %sG%d_0 + gl0[(i64)e * L0DIM + %d + uc];",
                             env ? "ev * " : "", b, q.l0_col);
-    std::map<std::pair<int, int>, std::vector<const Term*>> by_ij;
-    for (const Term& t : q.terms) by_ij[{t.i, t.j}].push_back(&t);
     std::set<int> is, js;
-    for (const auto& kv : by_ij) {
-      is.insert(kv.first.first);
-      js.insert(kv.first.second);
+    for (const Term& t : q.terms) {
+      is.insert(t.i);
+      js.insert(t.j);
     }
     for (int j : js) c.line("        real b%d = 0;", j);
     for (int i : is) c.line("        real a%d = 0;", i);
     // Pairs whose coefficient vectors over k agree up to sign share one q
     // (the signed coefficient classes of src/lunatp/utils/layout.py:110-168).
-    std::vector<SignedClass> classes = signed_classes(by_ij);
-    for (size_t n = 0; n < classes.size(); ++n) {
-      const SignedClass& cls = classes[n];
-      bool first = true;
-      for (const auto& kc : cls.coefficients) {
-        std::string coef = literal(kc.second, bits);
-        std::string seed = scalar_seed ? std::string("S0") : "G" + std::to_string(b) + "_" + std::to_string(kc.first);
-        if (first) {
-          c.line("        real q%zu = %s * %s;", n, coef.c_str(), seed.c_str());
-          first = false;
-        } else {
-          c.line("        q%zu = FMA(%s, %s, q%zu);", n, coef.c_str(), seed.c_str(), n);
+    const std::vector<SignedClass>& classes = path_classes[n];
+    for (size_t m = 0; m < classes.size(); ++m) {
+      const SignedClass& cls = classes[m];
+      const auto h = hoisted.find({n, m});
+      if (h != hoisted.end()) {
+        c.line("        const real q%zu = %s;", m, h->second.c_str());
+      } else {
+        bool first = true;
+        for (const auto& kc : cls.coefficients) {
+          std::string coef = literal(kc.second, bits);
+          std::string seed =
+              scalar_seed ? std::string("S0") : "G" + std::to_string(b) + "_" + std::to_string(kc.first);
+          if (first) {
+            c.line("        real q%zu = %s * %s;", m, coef.c_str(), seed.c_str());
+            first = false;
+          } else {
+            c.line("        q%zu = FMA(%s, %s, q%zu);", m, coef.c_str(), seed.c_str(), m);
+          }
         }
       }
       for (const auto& member : cls.members) {
         const int i = member.i, j = member.j;
         const char* sign = member.sign > 0 ? "" : "-";
-        c.line("        b%d = FMA(%sx%d, q%zu, b%d);", j, sign, i, n, j);
+        c.line("        b%d = FMA(%sx%d, q%zu, b%d);", j, sign, i, m, j);
         ycopy.need(c, q.y_off + j);
-        c.line("        a%d = FMA(%sy%d, q%zu, a%d);", i, sign, q.y_off + j, n, i);
+        c.line("        a%d = FMA(%sy%d, q%zu, a%d);", i, sign, q.y_off + j, m, i);
       }
     }
     // gw = sum_i x_i a_i  (= sum_ij x_i y_j q_ij)
