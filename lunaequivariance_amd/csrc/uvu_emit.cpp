@@ -64,6 +64,8 @@ struct Options {
   bool y_vgpr = true;    // copy y into vector registers before use: a scalar
                          // operand makes a VALU op issue at half rate
   bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
+  int lds_reduce = -1;   // gy partials summed over the 64 lanes through LDS (1) or by a
+                         // butterfly of lane exchanges (0); -1: LDS for fp64
   int hoist_regs = -1;   // registers the backward may spend on q classes computed once
                          // per node instead of per edge (-1: by precision)
   int fwd_local = 0;     // forward in per-path form (no products shared between
@@ -99,6 +101,7 @@ Options options() {
   o.bwd_prefetch = value("bpre", o.bwd_prefetch);
   o.hoist = value("hoist", o.hoist) != 0;
   o.hoist_regs = value("hq", o.hoist_regs);
+  o.lds_reduce = value("lred", o.lds_reduce);
   o.fwd_wpe = value("fwpe", o.fwd_wpe);
   o.bwd_wpe = value("bwpe", o.bwd_wpe);
   o.out_lds = value("olds", o.out_lds) != 0;
@@ -211,6 +214,34 @@ std::string emit_butterfly(Code& c, std::vector<std::string> names, const char* 
   *shift = 6 - split_bits;
   *low_mask = (1 << (6 - split_bits)) - 1;
   return names[0];
+}
+
+// Odd row pitch of the per-wave LDS transpose of n partial values.
+int reduce_pitch(int n) { return n % 2 ? n + 2 : n + 1; }
+
+// The same reduction through LDS: every lane writes its n values as one row
+// of a per-wave 64 x n table, then L lanes per column each add 64 / L rows
+// and lane exchanges within the L finish the sum (fewer VALU instructions
+// than the butterfly's selects, which in fp64 are two per value).  Lane L
+// then holds column L >> shift, as with emit_butterfly.
+std::string emit_lds_reduce(Code& c, const std::vector<std::string>& names, const char* prefix, int* shift,
+                            int* low_mask) {
+  const int n = (int)names.size(), pitch = reduce_pitch(n);
+  int cols = 1;
+  while (cols < n) cols *= 2;
+  const int lanes = 64 / cols, rows = 64 / lanes;
+  for (int v = 0; v < n; ++v) c.line("        red[lane * %d + %d] = %s;", pitch, v, names[v].c_str());
+  c.line("        asm volatile(\"\" ::: \"memory\");");
+  c.line("        const int %sc = min(lane / %d, %d), %sp = lane %% %d;", prefix, lanes, n - 1, prefix, lanes);
+  c.line("        real %ss = red[%sp * %d + %sc];", prefix, prefix, pitch, prefix);
+  for (int r = 1; r < rows; ++r)
+    c.line("        %ss += red[(%sp + %d) * %d + %sc];", prefix, prefix, r * lanes, pitch, prefix);
+  for (int m = lanes / 2; m >= 1; m /= 2) c.line("        %ss += xchg<%d>(%ss);", prefix, m, prefix);
+  int bits = 0;
+  while ((1 << bits) < lanes) ++bits;
+  *shift = bits;
+  *low_mask = lanes - 1;
+  return std::string(prefix) + "s";
 }
 
 // (i, j) pairs of one path grouped by their coefficient vector over k, equal
@@ -566,6 +597,7 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
   const int np = (int)g.paths.size();
+  const bool lds_reduce = opt.lds_reduce < 0 ? bits == 64 : opt.lds_reduce != 0;
   if (g.subsets > 1)
     c.line("    const int u = ((slot - %d) / %d) * 64 + lane;", g.slot_base, g.subsets);
   else
@@ -682,7 +714,8 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     c.line("      {");
     for (const auto& v : values) c.line("        %s = active ? %s : (real)0;", v.c_str(), v.c_str());
     int shift = 0, low = 0;
-    std::string total = emit_butterfly(c, values, tag.c_str(), &shift, &low);
+    std::string total = lds_reduce ? emit_lds_reduce(c, values, tag.c_str(), &shift, &low)
+                                   : emit_butterfly(c, values, tag.c_str(), &shift, &low);
     c.line("        const int col = lane >> %d;", shift);
     c.line("        const bool own = (lane & %d) == 0 && col < %zu;", low, values.size());
     if (g.pair_partials) {
@@ -962,6 +995,16 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     bool pairs = false;
     for (const Group& g : plan.bwd_groups) pairs = pairs || (g.phase == phase && g.pair_partials);
     if (pairs && want_part) c.line("  __shared__ real gy_share[2][PART_W];");
+    if (want_part && (opt.lds_reduce < 0 ? spec.dtype_bits == 64 : opt.lds_reduce != 0)) {
+      // Per-wave table of the LDS reduction of the gy partials.
+      int most = 1;
+      for (const Group& g : plan.bwd_groups)
+        if (g.phase == phase) most = std::max(most, (int)group_use(spec, g).ys.size() + (env ? 1 : 0));
+      const int pitch = reduce_pitch(most);
+      c.line("  __shared__ real red_lds[%d];", std::max(waves, 1) * 64 * pitch);
+      c.line("  real* const red = red_lds + %s * %d;",
+             waves > 0 ? "__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)" : "0", 64 * pitch);
+    }
     if (waves == 0) {
       // One wave per workgroup, the slots of a node on consecutive workgroups.
       c.line("  const int lane = threadIdx.x;");
