@@ -1060,6 +1060,32 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   c.line("  const int t = threadIdx.x;");
   c.line("  const i64 e0 = (i64)blockIdx.x * 256;");
   c.line("  const int n = E - e0 < 256 ? (int)(E - e0) : 256;");
+  // When every slot holds every column in place (each group reads every y
+  // component), the sum is element-wise over the slots' runs: every thread
+  // adds the same element of all slots, with all their loads in flight.
+  bool in_place = !by_slot.empty() && pw == (int)spec.in2 + (env ? 1 : 0);
+  for (const auto& kv : by_slot) {
+    in_place = in_place && (int)kv.second.size() == pw;
+    for (const auto& pc : kv.second) in_place = in_place && pc.first == pc.second;
+  }
+  if (in_place) {
+    c.line("  #pragma unroll 4");
+    c.line("  for (int i = t; i < n * (int)PART_W; i += 256) {");
+    bool first = true;
+    for (const auto& kv : by_slot) {
+      c.line("    %s part[((i64)%d * E + e0) * PART_W + i];", first ? "real v =" : "v +=", kv.first);
+      first = false;
+    }
+    c.line("    tile[i] = v;");
+    c.line("  }");
+    c.line("  __syncthreads();");
+    c.line("  if (gy) {");
+    c.line("    real* dst = gy + e0 * IN2;");
+    c.line("    for (int i = t; i < n * (int)IN2; i += 256) dst[i] = tile[(i / IN2) * PART_W + i %% IN2];");
+    c.line("  }");
+    if (env) c.line("  if (genv && t < n) genv[e0 + t] = tile[t * PART_W + IN2];");
+    c.line("}");
+  } else {
   for (int col = 0; col < pw; ++col) c.line("  real acc%d = 0;", col);
   // Consecutive slots with the same column map (the chunks of one group) share
   // one loop, so the code size does not grow with the channel count.
@@ -1091,6 +1117,7 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   c.line("  }");
   if (env) c.line("  if (genv && t < n) genv[e0 + t] = acc%d;", spec.in2);
   c.line("}");
+  }
   c.line("extern \"C\" __global__ void __launch_bounds__(256) luna_uvu_fill(real* __restrict__ p, i64 n) {");
   c.line("  const i64 i = (i64)blockIdx.x * 256 + threadIdx.x;");
   c.line("  if (i < n) p[i] = 0;");
