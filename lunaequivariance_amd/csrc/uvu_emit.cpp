@@ -592,8 +592,11 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
 // kernel sums the messages over each source node's out-edges.
 // One wave's share of a backward group: all of its paths, or one subset of
 // a split group (`g` is then the subset's view, sub its index).
+Group subset_view(const Group& g, int sub);
+
 void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
-                        bool want_msg, bool want_part, const Options& opt, int sub, bool cmajor) {
+                        bool want_msg, bool want_part, const Options& opt, int sub, bool cmajor,
+                        const Group* whole) {
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
   const int np = (int)g.paths.size();
@@ -689,6 +692,23 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
       if (left[name] > 0) resident.push_back(name);
     for (const auto& kv : hoisted) resident.push_back(kv.second);
     seeds = resident;
+  }
+  // Combined subsets: lane c of the first subset's wave adds column c (y
+  // index, env last) of both subsets' partials; r0 / r1 are that column's
+  // positions in the two subsets' value lists (-1: not there).
+  const bool combine = whole && whole->combine_subsets && want_part;
+  if (combine && sub == 0) {
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const GroupUse other = group_use(spec, subset_view(*whole, s2));
+      std::string chain = "-1";
+      int rank = 0;
+      std::vector<std::pair<int, int>> ranks;
+      for (int yi : other.ys) ranks.push_back({yi, rank++});
+      if (env) ranks.push_back({(int)spec.in2, rank});
+      for (auto it = ranks.rbegin(); it != ranks.rend(); ++it)
+        chain = "lane == " + std::to_string(it->first) + " ? " + std::to_string(it->second) + " : (" + chain + ")";
+      c.line("    const int r%d = %s;", s2, chain.c_str());
+    }
   }
   auto body = [&]() {
   if (!opt.hoist) {
@@ -832,17 +852,38 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     for (int i : is) c.line("        M%d = FMA(ws, a%d, M%d);", i, i, i);
     c.line("      }");
   }
-  if (want_msg && g.subsets > 1) {
+  std::vector<std::string> values;
+  for (int yi : use.ys) values.push_back("GY" + std::to_string(yi));
+  if (env) values.push_back("GE");
+  // gy partials of a combined subset: reduced over the lanes and left in LDS
+  // (the second subset's before the barrier, the first's after it, each after
+  // its message work so that the message values are dead by then).
+  auto reduce_to_lds = [&]() {
+    c.line("      {");
+    for (const auto& v : values) c.line("        %s = active ? %s : (real)0;", v.c_str(), v.c_str());
+    int shift = 0, low = 0;
+    const std::string tag = "s" + std::to_string(sub) + "_";
+    std::string total = lds_reduce ? emit_lds_reduce(c, values, tag.c_str(), &shift, &low)
+                                   : emit_butterfly(c, values, tag.c_str(), &shift, &low);
+    c.line("        const int col = lane >> %d;", shift);
+    c.line("        if ((lane & %d) == 0 && col < %zu) gy_sub[%d][(e - beg) & 1][col] = %s;", low, values.size(), sub,
+           total.c_str());
+    c.line("      }");
+  };
+  if ((want_msg || combine) && g.subsets > 1) {
     // The second subset hands its message share to the first through LDS
     // (two buffers by edge parity: one barrier per edge orders both uses).
     c.line("      {");
     c.line("        const int par = (e - beg) & 1;");
     if (sub == 1) {
-      for (int i = 0; i < g.d1; ++i) c.line("        msg_share[par][%d][lane] = M%d;", i, i);
+      if (want_msg)
+        for (int i = 0; i < g.d1; ++i) c.line("        msg_share[par][%d][lane] = M%d;", i, i);
+      if (combine) reduce_to_lds();
       c.line("        __syncthreads();");
     } else {
       c.line("        __syncthreads();");
-      for (int i = 0; i < g.d1; ++i) c.line("        M%d += msg_share[par][%d][lane];", i, i);
+      if (want_msg)
+        for (int i = 0; i < g.d1; ++i) c.line("        M%d += msg_share[par][%d][lane];", i, i);
     }
     c.line("      }");
   }
@@ -868,10 +909,18 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     }
     c.line("      }");
   }
-  std::vector<std::string> values;
-  for (int yi : use.ys) values.push_back("GY" + std::to_string(yi));
-  if (env) values.push_back("GE");
-  flush(values);
+  if (combine && sub == 0) {
+    reduce_to_lds();
+    c.line("      {");
+    c.line("        const int par = (e - beg) & 1;");
+    c.line("        if (r0 >= 0 || r1 >= 0)");
+    c.line("          part[((i64)(%d + (slot - %d) / 2) * E + e) * PART_W + lane] =", whole->gy_slot_base,
+           whole->slot_base);
+    c.line("              (r0 >= 0 ? gy_sub[0][par][r0 < 0 ? 0 : r0] : (real)0) +");
+    c.line("              (r1 >= 0 ? gy_sub[1][par][r1 < 0 ? 0 : r1] : (real)0);");
+    c.line("      }");
+  }
+  if (!combine) flush(values);
   };
   emit_edge_loop(c, spec, g, use, env, opt, seeds, body);
 }
@@ -899,13 +948,14 @@ Group subset_view(const Group& g, int sub) {
 void emit_backward_group(Code& c, const Spec& spec, const Group& g, bool env, bool gl0, bool want_gw,
                          bool want_msg, bool want_part, const Options& opt, bool cmajor) {
   if (g.subsets == 1) {
-    emit_backward_wave(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt, 0, cmajor);
+    emit_backward_wave(c, spec, g, env, gl0, want_gw, want_msg, want_part, opt, 0, cmajor, nullptr);
     return;
   }
   c.line("    const int sub = (slot - %d) %% %d;", g.slot_base, g.subsets);
   for (int sub = 0; sub < g.subsets; ++sub) {
     c.line("    %sif (sub == %d) {", sub ? "else " : "", sub);
-    emit_backward_wave(c, spec, subset_view(g, sub), env, gl0, want_gw, want_msg, want_part, opt, sub, cmajor);
+    emit_backward_wave(c, spec, subset_view(g, sub), env, gl0, want_gw, want_msg, want_part, opt, sub, cmajor,
+                       &g);
     c.line("    }");
   }
 }
@@ -995,6 +1045,9 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     bool pairs = false;
     for (const Group& g : plan.bwd_groups) pairs = pairs || (g.phase == phase && g.pair_partials);
     if (pairs && want_part) c.line("  __shared__ real gy_share[2][PART_W];");
+    bool combined = false;
+    for (const Group& g : plan.bwd_groups) combined = combined || (g.phase == phase && g.combine_subsets);
+    if (combined && want_part) c.line("  __shared__ real gy_sub[2][2][PART_W];");
     if (want_part && (opt.lds_reduce < 0 ? spec.dtype_bits == 64 : opt.lds_reduce != 0)) {
       // Per-wave table of the LDS reduction of the gy partials.
       int most = 1;
@@ -1036,6 +1089,15 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
   const int pw = spec.in2 + (env ? 1 : 0);
   std::vector<std::vector<std::pair<int, int>>> writers(pw);
   for (const Group& g : plan.bwd_groups) {
+    if (g.combine_subsets) {
+      // One slot per chunk, columns in place (y index, env last).
+      const GroupUse use = group_use(spec, g);
+      for (int chunk = 0; chunk < g.chunks; ++chunk) {
+        for (int yi : use.ys) writers[yi].push_back({g.gy_slot_base + chunk, yi});
+        if (env) writers[spec.in2].push_back({g.gy_slot_base + chunk, (int)spec.in2});
+      }
+      continue;
+    }
     for (int sub = 0; sub < g.subsets; ++sub) {
       GroupUse use = group_use(spec, g.subsets > 1 ? subset_view(g, sub) : g);
       for (int chunk = 0; chunk < g.chunks; ++chunk) {

@@ -55,6 +55,9 @@ struct Group {
   // Backward: the group's two 64-channel chunks run as the two waves of one
   // workgroup and add their gy partials through LDS into one slot.
   bool pair_partials = false;
+  // Split group whose two path subsets (the two waves of a workgroup) add
+  // their gy partials through LDS into one slot per chunk, columns in place.
+  bool combine_subsets = false;
   // Backward: the paths may be split into `subsets` path sets, each run by
   // its own wave (slot = chunk * subsets + subset); the two waves of a split
   // group share a workgroup and sum their gx messages through LDS.

@@ -389,8 +389,9 @@ void build_schedule(Plan& plan) {
   for (Group& g : plan.bwd_groups) {
     g.pair_partials = pair && g.subsets == 1 && g.chunks == 2 && g.slot_base % 2 == 0 &&
                       plan.bwd_block_waves[g.phase] == 2;
+    g.combine_subsets = pair && g.subsets == 2 && plan.bwd_block_waves[g.phase] == 2;
     g.gy_slot_base = parts;
-    parts += g.pair_partials ? 1 : g.chunks * g.subsets;
+    parts += g.pair_partials ? 1 : g.combine_subsets ? g.chunks : g.chunks * g.subsets;
   }
   plan.gy_parts = parts;
   for (int s : slots)

@@ -128,14 +128,14 @@ def test_product_path_has_no_cpu_fallback():
 
 def test_fp64_backward_splits_large_groups():
     """fp64 backward groups holding more than 24 output seeds run as two path
-    subsets, each with its own gy partial slot per channel chunk; fp32 keeps one
-    wave per group and chunk, and the two chunk waves of a group share one
-    partial slot (they add their partials in LDS)."""
+    subsets that add their gy partials in LDS into one slot per channel chunk;
+    fp32 keeps one wave per group and chunk, and the two chunk waves of a group
+    share one partial slot (they add their partials in LDS)."""
     # lmax=3, 128 channels: input blocks l=0..3 hold 16, 39, 51, 50 seeds.
     f32 = op_for(channels=128, lmax=3, dtype=torch.float32).plan.info
     f64 = op_for(channels=128, lmax=3, dtype=torch.float64).plan.info
     assert f32.gy_parts == 4
-    assert f64.gy_parts == 1 + 3 * 2 * 2
+    assert f64.gy_parts == 1 + 3 * 2
 
 
 def test_graph_entry_points_check_arguments():
