@@ -61,8 +61,10 @@ struct Options {
   bool nt_w = false;     // the setting of the kernel being emitted
   bool nt_gw = true;     // non-temporal stores of the weight gradient
   int nt_msg = -1;       // non-temporal stores of the gx messages (-1: as bwd_nt_w)
-  bool y_vgpr = true;    // copy y into vector registers before use: a scalar
-                         // operand makes a VALU op issue at half rate
+  int y_vgpr = -1;       // copy y into vector registers before use: a scalar
+                         // operand makes an fp32 VALU op issue at half rate
+                         // (-1: fp32 only; fp64 without the copies measured
+                         // forward 9.7 -> 8.9 ms, backward unchanged)
   bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
   int lds_reduce = -1;   // gy partials summed over the 64 lanes through LDS (1) or by a
                          // butterfly of lane exchanges (0); -1: LDS for fp64
@@ -96,7 +98,7 @@ Options options() {
   o.bwd_nt_w = value("bntw", o.bwd_nt_w);
   o.nt_gw = value("ntgw", o.nt_gw) != 0;
   o.nt_msg = value("ntmsg", o.nt_msg);
-  o.y_vgpr = value("yv", o.y_vgpr) != 0;
+  o.y_vgpr = value("yv", o.y_vgpr);
   o.fwd_local = value("flocal", o.fwd_local);
   o.bwd_prefetch = value("bpre", o.bwd_prefetch);
   o.hoist = value("hoist", o.hoist) != 0;
@@ -475,7 +477,7 @@ void emit_forward_group(Code& c, const Spec& spec, const Group& g, bool env, boo
     return spec.paths[g.paths[a]].y_off < spec.paths[g.paths[b]].y_off;
   });
   std::set<std::pair<int, int>> formed;
-  YCopies ycopy{opt.y_vgpr, {}};
+  YCopies ycopy{opt.y_vgpr < 0 ? spec.dtype_bits == 32 : opt.y_vgpr != 0, {}};
   for (int n : order) {
     const Path& q = spec.paths[g.paths[n]];
     const int b = g.path_block[n];
@@ -716,7 +718,7 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     // instead of holding all of them in registers across it.
     for (const auto& name : seeds) c.line("      asm volatile(\"\" : \"+v\"(%s));", name.c_str());
   }
-  YCopies ycopy{opt.y_vgpr, {}};
+  YCopies ycopy{opt.y_vgpr < 0 ? spec.dtype_bits == 32 : opt.y_vgpr != 0, {}};
   for (int i = 0; i < g.d1; ++i) c.line("      real M%d = 0;", i);
   for (int yi : use.ys) c.line("      real GY%d = 0;", yi);
   if (env) c.line("      real GE = 0;");
