@@ -325,6 +325,22 @@ def test_full_size_sampled_rows(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_lmax3_split_groups_with_envelope_and_scalar_features(dtype):
+    """The lmax-3 layout, whose fp64 backward splits input blocks into two path
+    subsets that combine their gy partials (env column included) in LDS, with an
+    envelope and the scalar-path features (gl0 enters the per-edge seeds)."""
+    in1, sh, out, instructions = mace_irreps(16, 3)
+    conv = make_conv(in1, sh, out, instructions, dtype)
+    gen = torch.Generator().manual_seed(33)
+    nodes, edges = 30, 200
+    src, dst = random_graph(nodes, edges, gen)
+    x, y, w = inputs(conv, nodes, edges, dtype, gen)
+    env = torch.rand(edges, 1, generator=gen, dtype=torch.float64)
+    check_orders(conv, in1, sh, out, instructions, x, y, w, src, dst, nodes, dtype, gen, env=env, l0=True,
+                 orders=2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_wide_mixed_width_edge_channels(dtype):
     """Blocks of 65,537 and 65,601 channels, several edge channels, a repeated
     instruction, env with zeros and scalar features (``tests/lunatp/test_uvu_conv.py:500-575``)."""
