@@ -247,3 +247,26 @@ def test_uvw_graph_capture_replays():
         for n, (a, b) in enumerate(zip(static, expected)):
             scale = b.abs().max()
             assert (a - b).abs().max() <= 1e-5 * scale + 1e-6, f"replay {replay}, output {n}"
+
+
+def test_uvw_row_block_fastest_grid(monkeypatch):
+    """The grid order the launches fall back to above 65,535 row blocks (row block
+    fastest, LUNAEQ_AMD_UVW_TF=0 forces it here): same results as the oracle."""
+    monkeypatch.setenv("LUNAEQ_AMD_UVW_TF", "0")
+    ir, sh = "64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e"
+    instructions = uvw_instructions(ir, sh, ir)
+    tp = lunaeq.TensorProduct(ir, sh, ir, instructions, shared_weights=True, internal_weights=False)
+    rows = 600
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+    y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+    w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64) / 8
+    ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+    ref = uvw_tensor_product(ir, sh, ir, instructions, *ref_in)
+    dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+    act = tp(*dev_in)
+    assert_close(act, ref, torch.float32, "forward")
+    g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    for n, (a, r) in enumerate(zip(torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32)),
+                                   torch.autograd.grad(ref, ref_in, g))):
+        assert_close(a, r, torch.float32, f"first-order {n}")
