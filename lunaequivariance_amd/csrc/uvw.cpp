@@ -57,6 +57,7 @@ struct UvwSpec {
   int wpad = 2;  // LUNAEQ_AMD_UVW_WPAD: weight-row padding (2: the A-operand reads conflict-free, as above)
   int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
   int wrows = 2;  // LUNAEQ_AMD_UVW_WROWS: batch rows per LDS copy of the weight gradient (2, or 4)
+  bool bdma = true;  // LUNAEQ_AMD_UVW_BDMA: gx/gy chunks copied by global_load_lds one chunk ahead (0: via registers)
 };
 
 constexpr int kChunkRows = 256;  // default batch rows per wave (and per partial) of the weight gradient
@@ -735,6 +736,16 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+// 16 bytes per lane from src to LDS at dst + 16 lane (dst uniform).  Issued as
+// asm so that the compiler does not wait for these copies before unrelated
+// LDS reads (it cannot tell the buffers apart); the kernel waits for them
+// itself (vmcnt 0) before the barrier that publishes a chunk.  Extra
+// outstanding loads only lengthen the compiler's own in-order vmcnt waits.
+// Nothing else in these kernels reads M0.
+__device__ __forceinline__ void lds_copy16(const void* src, lvoid* dst) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"((unsigned)(size_t)dst) : "memory");
+}
 )";
   for (int phase = 0; phase < phases; ++phase) {
     // Four waves per SIMD when the per-lane state is small (short waves whose
@@ -758,33 +769,44 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       const int estimate = 8 * head.d1 + 4 * d3 + 2 * (int)ycols.size() + 48;
       if (estimate > 128) four = false;
     }
-    c.line("extern \"C\" __global__ void __launch_bounds__(256) %sluna_uvw_bwd_xy_p%d(",
-           four ? "__attribute__((amdgpu_waves_per_eu(4))) " : "__attribute__((amdgpu_waves_per_eu(2))) ", phase);
     const bool cy_form = s.bcy < 0 ? four : s.bcy != 0;
-    c.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
-    c.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B, int tf) {");
-    c.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
-    emit_grid_order(c);
     int stage_d3 = 0, cw = s.bcw;  // w per staged chunk
+    bool dma = s.bdma;
     for (const Unit& u : units)
       if (u.phase == phase)
         for (int p : u.paths)
           if (staged_seeds(s, s.paths[p])) {
             stage_d3 = std::max(stage_d3, s.paths[p].d3);
             if (s.paths[p].mul3 % cw) cw = 16;
+            // Copied rows cannot be zeroed: every K row of the tiles must exist.
+            if (s.paths[p].mul1 * s.paths[p].mul2 % 16) dma = false;
           }
+    dma = dma && stage_d3;
+    Code kc;  // the kernel up to the unit bodies
+    kc.line("extern \"C\" __global__ void __launch_bounds__(256) %sluna_uvw_bwd_xy_p%d(",
+            four ? "__attribute__((amdgpu_waves_per_eu(4))) " : "__attribute__((amdgpu_waves_per_eu(2))) ", phase);
+    kc.line("    const real* __restrict__ x, const real* __restrict__ y, const real* __restrict__ wt,");
+    kc.line("    const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part, int B, int tf) {");
+    kc.line("  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;");
+    emit_grid_order(kc);
     // The four waves of a workgroup take four K tiles of one input block for
     // the same 16 batch rows and share the staged seed rows.
-    if (stage_d3) {
-      c.line("  __shared__ __attribute__((aligned(16))) real gs[2][16][%d];", cw * stage_d3 + s.gpad);
-      c.line("  __shared__ real wsh[4][16][%d];", cw + s.wpad);
-      c.line("  int chunk = 0;");
+    if (dma) {
+      kc.line("  __shared__ __attribute__((aligned(16))) real gsd[2][%d];", 16 * cw * stage_d3);
+      kc.line("  __shared__ __attribute__((aligned(16))) real wsd[2][4][%d];", 16 * cw);
+    } else if (stage_d3) {
+      kc.line("  __shared__ __attribute__((aligned(16))) real gs[2][16][%d];", cw * stage_d3 + s.gpad);
+      kc.line("  __shared__ real wsh[4][16][%d];", cw + s.wpad);
+      kc.line("  int chunk = 0;");
     }
-    c.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
-    c.line("  const int b0 = rb * 16;");
-    c.line("  if (b0 >= B) return;");
-    c.line("  const bool rok = b0 + c16 < B;");
-    c.line("  const int brow = rok ? b0 + c16 : B - 1;");
+    kc.line("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
+    kc.line("  const int b0 = rb * 16;");
+    kc.line("  if (b0 >= B) return;");
+    kc.line("  const bool rok = b0 + c16 < B;");
+    kc.line("  const int brow = rok ? b0 + c16 : B - 1;");
+    Code ub;  // the unit bodies
+    {
+    Code& c = ub;
     c.line("  int unit = ut;");
     for (const Unit& un : units) {
       if (un.phase != phase) continue;
@@ -805,6 +827,36 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       c.line("    const int ka = kt * 16 + c16;");  // A operand row (K index) of this lane
       c.line("    const bool kaok = ka < %d;", Ktot);
       c.line("    const int kb = kt * 16 + 4 * grp;");  // first of this lane's four D rows
+      // Copied chunks: 16-byte piece pc of batch (or K) row r of a chunk lands
+      // in LDS slot 16 pc + r (lane l of copy instruction j fills slot
+      // 64 j + l), so a lane's reads of its row across the 16 rows of a tile
+      // fall in distinct banks.  The seed pieces are shared by the workgroup
+      // (instruction j issued by wave j % 4; waves past the last instruction
+      // repeat it, the same bytes to the same place, rather than branch);
+      // each wave copies its own 16 W rows.
+      std::vector<std::pair<int, int>> items;  // (path, chunk) in order
+      int item = 0;
+      auto dma_copy = [&](int t) {
+        const UvwPath& q = s.paths[items[t].first];
+        const int cn = items[t].second, par = t & 1, nj = cw * q.d3 / 16;
+        for (int i = 0; 4 * i < nj; ++i) {
+          const std::string j = 4 * i + 4 <= nj ? "wave" : "min(wave, " + std::to_string(nj - 4 * i - 1) + ")";
+          c.line("    lds_copy16(grow + %d + 16 * %s, (lvoid*)(G%d + %d + 256 * %s));", q.out_off + cn * cw * q.d3 + 64 * i,
+                 j.c_str(), par, 1024 * i, j.c_str());
+        }
+        for (int j = 0; j < cw / 16; ++j)
+          c.line("    lds_copy16(wt + (i64)ka * %d + %d + 4 * grp, (lvoid*)(W%d + %d));", q.mul3, q.w_off + cn * cw + 16 * j,
+                 par, 256 * j);
+      };
+      if (dma) {
+        for (int p : un.paths)
+          if (staged_seeds(s, s.paths[p]))
+            for (int cn = 0; cn < s.paths[p].mul3 / cw; ++cn) items.push_back({p, cn});
+        if (!items.empty()) {
+          c.line("    const real* grow = g + (i64)brow * %d + 4 * grp;", s.out);
+          dma_copy(0);
+        }
+      }
       for (int qd = 0; qd < nq; ++qd)
         for (int i = 0; i < d1; ++i) c.line("    real gxa%d_%d = 0;", qd, i);
       for (const auto& kv : cols) c.line("    real %s = 0;", kv.second.c_str());
@@ -847,7 +899,36 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
         for (int v = 0; v < m2; ++v)
           for (int j : js) c.line("      real gp%d_%d = 0;", v, j);
         for (int k = 0; k < d3; ++k) c.line("      floatx4 dz%d = (floatx4)(0.0f);", k);
-        if (vec) {
+        if (vec && dma) {
+          // Wait for this chunk's copies (all of this wave's copies in flight),
+          // make the workgroup's visible, request the next chunk into the
+          // other buffers, then the matrix work on this one.  Lane group grp
+          // contracts w = 4 ss + grp: A at slot 16 ss + c16, offset grp; B
+          // element f = (4 ss + grp) d3 + k of row c16 at slot 16 (f / 4) + c16,
+          // offset f % 4, through per-lane bases bq[(k % 4)] (grp d3 mod 4
+          // differs across the groups: no bank conflicts).
+          c.line("      const int gq = grp * %d;", d3);
+          for (int c0 = 0; c0 < std::min(4, d3); ++c0)
+            c.line("      const int bq%d = 64 * ((gq + %d) >> 2) + c16 * 4 + ((gq + %d) & 3);", c0, c0, c0);
+          for (int cn = 0; cn < mul3 / cw; ++cn, ++item) {
+            const int par = item & 1;
+            c.line("      {");
+            c.line("        __builtin_amdgcn_s_waitcnt(%d);", vmcnt_imm(0));
+            c.line("        asm volatile(\"\" ::: \"memory\");");
+            c.line("        __builtin_amdgcn_sched_barrier(0);");
+            c.line("        __syncthreads();");
+            if (item + 1 < (int)items.size()) dma_copy(item + 1);
+            c.line("        const lreal* al = W%d + c16 * 4 + grp;", par);
+            for (int ss = 0; ss < cw / 4; ++ss) {
+              c.line("        {");
+              c.line("          const real a = al[%d];", 64 * ss);
+              for (int k = 0; k < d3; ++k)
+                c.line("          dz%d = mfma16(a, G%d[bq%d + %d], dz%d);", k, par, k & 3, 64 * (ss * d3 + (k >> 2)), k);
+              c.line("        }");
+            }
+            c.line("      }");
+          }
+        } else if (vec) {
           // Chunks of cw w: the seed rows of the 16 batch rows and the W rows
           // of the 16 K indices go through LDS, read from HBM / L2 with
           // consecutive lanes on consecutive addresses; within a chunk lane
@@ -974,8 +1055,24 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
       for (const auto& kv : cols) c.line("        pr[%d] = %s;", kv.first, kv.second.c_str());
       c.line("      }");
       c.line("    }");
+      // The next K tiles' first copy reuses buffer 0.
+      if (dma && kts > 4 && !items.empty()) c.line("    __syncthreads();");
       c.line("  }");
       c.line("  unit -= 1;");
+    }
+    }
+    if (dma) {
+      c.line("__device__ __forceinline__ void bxy_units_%d(const real* __restrict__ x, const real* __restrict__ y,", phase);
+      c.line("    const real* __restrict__ wt, const real* __restrict__ g, real* __restrict__ gx, real* __restrict__ part,");
+      c.line("    int B, int lane, int grp, int c16, int wave, int b0, bool rok, int brow, int ut,");
+      c.line("    lreal* __restrict__ G0, lreal* __restrict__ G1, lreal* __restrict__ W0, lreal* __restrict__ W1) {");
+      c.s << ub.s.str();
+      c.line("}");
+      c.s << kc.s.str();
+      c.line("  bxy_units_%d(x, y, wt, g, gx, part, B, lane, grp, c16, wave, b0, rok, brow, ut, (lreal*)&gsd[0][0],", phase);
+      c.line("              (lreal*)&gsd[1][0], (lreal*)&wsd[0][wave][0], (lreal*)&wsd[1][wave][0]);");
+    } else {
+      c.s << kc.s.str() << ub.s.str();
     }
     c.line("}");
   }
@@ -1398,6 +1495,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     }
     if (const char* wp = std::getenv("LUNAEQ_AMD_UVW_WPAD")) p.spec.wpad = std::atoi(wp) == 1 ? 1 : 2;
     if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
+    if (const char* bd = std::getenv("LUNAEQ_AMD_UVW_BDMA")) p.spec.bdma = std::atoi(bd) != 0;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
     p.kernels.tag = "uvw";
