@@ -57,7 +57,13 @@ struct UvwSpec {
   int wpad = 2;  // LUNAEQ_AMD_UVW_WPAD: weight-row padding (2: the A-operand reads conflict-free, as above)
   int bcw = 32;  // LUNAEQ_AMD_UVW_BCW: w per staged chunk of the gx/gy kernel (32, or 16)
   int wrows = 2;  // LUNAEQ_AMD_UVW_WROWS: batch rows per LDS copy of the weight gradient (2, or 4)
-  bool bdma = true;  // LUNAEQ_AMD_UVW_BDMA: gx/gy chunks copied by global_load_lds one chunk ahead (0: via registers)
+  // LUNAEQ_AMD_UVW_BDMA: gx/gy chunks copied by global_load_lds one chunk
+  // ahead (1) or staged through registers (0); -1: copied in the kernels
+  // whose per-lane state leaves two waves per SIMD, where the freed registers
+  // pay (degree-3 layer 1.517 -> 1.457 ms), staged where four fit (config 5:
+  // 0.771 against 0.781 ms, the copies' 16-byte pieces cannot be padded
+  // against the two-way bank conflicts of the B reads).
+  int bdma = -1;
 };
 
 constexpr int kChunkRows = 256;  // default batch rows per wave (and per partial) of the weight gradient
@@ -771,7 +777,7 @@ __device__ __forceinline__ void lds_copy16(const void* src, lvoid* dst) {
     }
     const bool cy_form = s.bcy < 0 ? four : s.bcy != 0;
     int stage_d3 = 0, cw = s.bcw;  // w per staged chunk
-    bool dma = s.bdma;
+    bool dma = s.bdma < 0 ? !four : s.bdma != 0;
     for (const Unit& u : units)
       if (u.phase == phase)
         for (int p : u.paths)
@@ -829,8 +835,8 @@ __device__ __forceinline__ void lds_copy16(const void* src, lvoid* dst) {
       c.line("    const int kb = kt * 16 + 4 * grp;");  // first of this lane's four D rows
       // Copied chunks: 16-byte piece pc of batch (or K) row r of a chunk lands
       // in LDS slot 16 pc + r (lane l of copy instruction j fills slot
-      // 64 j + l), so a lane's reads of its row across the 16 rows of a tile
-      // fall in distinct banks.  The seed pieces are shared by the workgroup
+      // 64 j + l), so the 16 rows of a tile read at one offset spread over 16
+      // banks.  The seed pieces are shared by the workgroup
       // (instruction j issued by wave j % 4; waves past the last instruction
       // repeat it, the same bytes to the same place, rather than branch);
       // each wave copies its own 16 W rows.
@@ -905,8 +911,9 @@ __device__ __forceinline__ void lds_copy16(const void* src, lvoid* dst) {
           // other buffers, then the matrix work on this one.  Lane group grp
           // contracts w = 4 ss + grp: A at slot 16 ss + c16, offset grp; B
           // element f = (4 ss + grp) d3 + k of row c16 at slot 16 (f / 4) + c16,
-          // offset f % 4, through per-lane bases bq[(k % 4)] (grp d3 mod 4
-          // differs across the groups: no bank conflicts).
+          // offset f % 4, through per-lane bases bq[(k % 4)].  A half-wave
+          // (32 banks) reads 16 rows at two offsets, so rows r and r + 8 share
+          // a bank: two-way conflicts, which 16-byte pieces cannot pad away.
           c.line("      const int gq = grp * %d;", d3);
           for (int c0 = 0; c0 < std::min(4, d3); ++c0)
             c.line("      const int bq%d = 64 * ((gq + %d) >> 2) + c16 * 4 + ((gq + %d) & 3);", c0, c0, c0);
@@ -1495,7 +1502,7 @@ int luna_uvw_plan_create(const char* spec, const char* cache_dir, LunaUvwPlan** 
     }
     if (const char* wp = std::getenv("LUNAEQ_AMD_UVW_WPAD")) p.spec.wpad = std::atoi(wp) == 1 ? 1 : 2;
     if (const char* bcw = std::getenv("LUNAEQ_AMD_UVW_BCW")) p.spec.bcw = std::atoi(bcw) == 16 ? 16 : 32;
-    if (const char* bd = std::getenv("LUNAEQ_AMD_UVW_BDMA")) p.spec.bdma = std::atoi(bd) != 0;
+    if (const char* bd = std::getenv("LUNAEQ_AMD_UVW_BDMA")) p.spec.bdma = std::atoi(bd) != 0 ? 1 : 0;
 
     p.kernels.cache_dir = cache_dir ? cache_dir : "";
     p.kernels.tag = "uvw";

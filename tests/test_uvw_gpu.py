@@ -270,3 +270,36 @@ def test_uvw_row_block_fastest_grid(monkeypatch):
     for n, (a, r) in enumerate(zip(torch.autograd.grad(act, dev_in, g.to(DEV, torch.float32)),
                                    torch.autograd.grad(ref, ref_in, g))):
         assert_close(a, r, torch.float32, f"first-order {n}")
+
+
+@pytest.mark.parametrize("copied", [0, 1])
+@pytest.mark.parametrize("in1,in2,out,rows", [
+    ("64x0e+64x1o+64x2e", "1x0e+1x1o+1x2e", "64x0e+64x1o+64x2e", 90),      # config 5 layer
+    ("96x0e+16x1o", "1x0e+2x1o", "48x0e+40x1o+8x2e", 70),                   # K > 64: two rounds of K tiles
+    ("16x0e+16x1o", "1x0e+1x1o", "64x0e+64x1o+16x2e", 45),                  # several chunks per path
+    ("64x0e+64x1o+64x2e+64x3o", "1x0e+1x1o+1x2e+1x3o", "64x0e+64x1o+64x2e+64x3o", 40),
+])
+def test_uvw_gx_gy_staging_modes(monkeypatch, copied, in1, in2, out, rows):
+    """gx and gy with the seed and weight chunks copied straight to LDS one chunk
+    ahead (LUNAEQ_AMD_UVW_BDMA=1) and staged through registers (0), whichever the
+    layout would pick by itself: both against the oracle."""
+    import lunaequivariance_amd.interface as itf
+    monkeypatch.setenv("LUNAEQ_AMD_UVW_BDMA", str(copied))
+    itf._cached.cache_clear()
+    try:
+        instructions = uvw_instructions(in1, in2, out)
+        tp = lunaeq.TensorProduct(in1, in2, out, instructions, shared_weights=True, internal_weights=False)
+        gen = torch.Generator().manual_seed(rows + copied)
+        x = torch.randn(rows, tp.irreps_in1.dim, generator=gen, dtype=torch.float64)
+        y = torch.randn(rows, tp.irreps_in2.dim, generator=gen, dtype=torch.float64)
+        w = torch.randn(tp.weight_numel, generator=gen, dtype=torch.float64) / 8
+        ref_in = [t.clone().requires_grad_() for t in (x, y, w)]
+        ref = uvw_tensor_product(in1, in2, out, instructions, *ref_in)
+        dev_in = [t.to(DEV, torch.float32).requires_grad_() for t in (x, y, w)]
+        act = tp(*dev_in)
+        g = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+        for n, (a, r) in enumerate(zip(torch.autograd.grad(act, dev_in[:2], g.to(DEV, torch.float32)),
+                                       torch.autograd.grad(ref, ref_in[:2], g))):
+            assert_close(a, r, torch.float32, f"{'gx' if n == 0 else 'gy'}, copied={copied}")
+    finally:
+        itf._cached.cache_clear()
