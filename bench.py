@@ -29,6 +29,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP64_PEAK_TFLOPS = 78.6
+FP32_VECTOR_PEAK_TFLOPS = 157.3
 
 CONFIGS = {
     "cfg2": dict(channels=128, atoms=20000, dtype="float32", double_backward=False),
@@ -103,7 +104,7 @@ def conv_flops(instructions, in1, in2, out, channels, E):
     Clebsch-Gordan term (x*y, times c, accumulate) plus 2 per output component
     (times w, accumulate).  The first-order backward does the same work twice
     (gx and gy/gw contractions of q = C g)."""
-    from oracle.wigner import wigner_3j
+    from lunaequivariance_amd.cg import wigner_3j
     import numpy as np
 
     total = 0
@@ -217,12 +218,15 @@ def main():
     step_bytes = sum(per_step.values())
     step_seconds = ms_per_step / 1000.0
     extra = {}
-    if dtype == torch.float64:
-        # FP64 roofline next to the HBM one: forward + first-order backward arithmetic.
-        flops = 3.0 * conv_flops(instructions, conv.irreps_in1, conv.irreps_in2, conv.irreps_out,
-                                 cfg["channels"], E)
-        extra["step_fp64_tflops"] = round(flops / step_seconds / 1e12, 2)
-        extra["step_fp64_frac"] = round(flops / step_seconds / 1e12 / FP64_PEAK_TFLOPS, 4)
+    # Vector-ALU roofline next to the HBM one: the arithmetic of the forward
+    # and of each backward launch (twice the forward's), against the fp64 or
+    # fp32 vector peak.
+    passes = 3.0 + (2.0 if cfg["double_backward"] else 0.0)
+    flops = passes * conv_flops(instructions, conv.irreps_in1, conv.irreps_in2, conv.irreps_out,
+                                cfg["channels"], E)
+    tag, peak = ("fp64", FP64_PEAK_TFLOPS) if dtype == torch.float64 else ("fp32", FP32_VECTOR_PEAK_TFLOPS)
+    extra[f"step_{tag}_tflops"] = round(flops / step_seconds / 1e12, 2)
+    extra[f"step_{tag}_frac"] = round(flops / step_seconds / 1e12 / peak, 4)
 
     cpu = None
     if not args.no_cpu_baseline:
