@@ -228,6 +228,9 @@ def main():
     extra[f"step_{tag}_tflops"] = round(flops / step_seconds / 1e12, 2)
     extra[f"step_{tag}_frac"] = round(flops / step_seconds / 1e12 / peak, 4)
 
+    from lunaequivariance_amd.placement import held_info
+    extra["workspace"] = held_info().get(device.index or 0, {"held": False})
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(in1, sh, out_irreps, instructions, x, y, w, g, src, dst, N, args.cpu_shard,

@@ -54,6 +54,11 @@ PROTOTYPES = {
     "luna_uuu_conv_bwd_workspace": (ctypes.c_int, [_VP, _I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_uuu_conv_bwd": (ctypes.c_int, [_VP] + [_VP] * 6 + [_I32P] * 4 + [_VP] * 5
                           + [ctypes.c_size_t, _I64, _I64, _VP]),
+    "luna_placed_alloc": (ctypes.c_int, [ctypes.c_size_t, _VP, ctypes.c_size_t, ctypes.c_size_t, _VP,
+                                          ctypes.POINTER(_VP), ctypes.POINTER(ctypes.c_int)]),
+    "luna_same_region": (ctypes.c_int, [_VP, ctypes.c_size_t, _VP, ctypes.c_size_t, _VP,
+                                         ctypes.POINTER(ctypes.c_int)]),
+    "luna_placed_free": (ctypes.c_int, [_VP]),
     "luna_graph_bounds": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _VP, _VP]),
     "luna_graph_workspace": (ctypes.c_int, [_I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
     "luna_graph_build": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _I64] + [_VP] * 15

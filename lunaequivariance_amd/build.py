@@ -13,7 +13,7 @@ import subprocess
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
-SOURCES = ["common.cpp", "uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp", "uvw.cpp", "graph.cpp", "uuu.cpp", "uvu_noalloc.hip"]
+SOURCES = ["common.cpp", "uvu_schedule.cpp", "uvu_emit.cpp", "uvu_runtime.cpp", "uvw.cpp", "graph.cpp", "uuu.cpp", "uvu_noalloc.hip", "placement.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wno-format-security",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

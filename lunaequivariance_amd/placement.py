@@ -1,0 +1,141 @@
+"""Per-device backward workspaces placed in another HBM region than the
+weight gradient they are written beside.
+
+The convolution backwards write the weight gradient and their per-edge gx
+messages at the same time.  Device memory on MI355X falls into regions of
+about 96 GB, and two buffers written together move about 25 % more bytes per
+second when they lie in different regions (config-2 backward 9.7 -> 8.7 ms
+with the message workspace away from the gradient; a 2 x 256 MB write probe
+tells the two cases apart).  A workspace of at least ``PLACE_MIN_BYTES`` is
+therefore held per device: ``luna_placed_alloc`` allocates it outside the
+region of the gradient buffer of the call that needs it, and every later
+call that fits in it reuses it.  A later call whose gradient buffer is new
+probes it once against the held workspace (``luna_same_region``; the probe
+overwrites part of the gradient buffer before the kernels fill it) and, if
+they share a region, places the workspace again, at most
+``MAX_REPLACEMENTS`` times per device.  Smaller workspaces, calls under HIP
+graph capture and ``LUNAEQ_AMD_PLACE=0`` use an ordinary stream-ordered
+torch allocation.
+
+The held buffer is ordered across streams by one event per device: a call
+waits for the previous call's work before it writes the buffer, and records
+its own.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+from . import _native
+
+PLACE_MIN_BYTES = 1 << 30
+PROBE_BYTES = 512 << 20  # what a probe overwrites of the gradient buffer
+MAX_REPLACEMENTS = 3
+
+
+def _enabled() -> bool:
+    return os.environ.get("LUNAEQ_AMD_PLACE", "1") != "0"
+
+
+def _spacer_budget() -> int:
+    return int(float(os.environ.get("LUNAEQ_AMD_PLACE_SPACER_GB", "128")) * (1 << 30))
+
+
+def _nbytes(tensor) -> int:
+    return tensor.numel() * tensor.element_size()
+
+
+class _Held:
+    """The placed buffer of a device, its last-use event and probe verdicts
+    ({gradient buffer address: shares the region})."""
+
+    def __init__(self, device: torch.device, nbytes: int, avoid, stream: int, replacements: int):
+        pointer, moved = ctypes.c_void_p(), ctypes.c_int()
+        avoid_ptr, avoid_bytes = (avoid.data_ptr(), _nbytes(avoid)) if avoid is not None else (None, 0)
+        with torch.cuda.device(device):
+            _native.check(_native.lib().luna_placed_alloc(nbytes, avoid_ptr, avoid_bytes, _spacer_budget(),
+                                                          stream, ctypes.byref(pointer), ctypes.byref(moved)),
+                          "luna_placed_alloc")
+        self.device, self.pointer, self.nbytes = device, pointer.value, nbytes
+        self.moved = bool(moved.value)
+        self.replacements = replacements
+        self.verdicts = {avoid_ptr: not self.moved} if avoid_ptr else {}
+        self.event = None
+
+    def shares_region(self, avoid, stream: int) -> bool:
+        key = avoid.data_ptr()
+        if key not in self.verdicts:
+            same = ctypes.c_int()
+            _native.check(_native.lib().luna_same_region(key, _nbytes(avoid), self.pointer, self.nbytes, stream,
+                                                         ctypes.byref(same)), "luna_same_region")
+            self.verdicts[key] = bool(same.value)
+        return self.verdicts[key]
+
+    def release(self) -> None:
+        if self.event is not None:
+            self.event.synchronize()
+        if self.pointer:
+            _native.check(_native.lib().luna_placed_free(self.pointer), "luna_placed_free")
+        self.pointer = None
+
+
+_lock = threading.Lock()
+_held: dict[int, _Held] = {}
+
+
+def run_with_workspace(device: torch.device, nbytes: int, avoid, launch) -> None:
+    """Call ``launch(pointer)`` with a device workspace of ``nbytes``.
+
+    ``avoid`` is the gradient the launch writes beside the workspace (a probe
+    may overwrite its first 512 MB before ``launch`` fills it) or None.
+    """
+    stream = torch.cuda.current_stream(device)
+    if not _enabled() or nbytes < PLACE_MIN_BYTES or torch.cuda.is_current_stream_capturing():
+        scratch = torch.empty(nbytes, device=device, dtype=torch.uint8)
+        launch(scratch.data_ptr())
+        return
+    if avoid is not None and (not avoid.is_contiguous() or _nbytes(avoid) < PROBE_BYTES):
+        avoid = None
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    with _lock:
+        held = _held.get(index)
+        if held is not None and held.event is not None:
+            stream.wait_event(held.event)
+        replace = held is None or held.nbytes < nbytes
+        if not replace and avoid is not None and held.replacements < MAX_REPLACEMENTS:
+            replace = held.shares_region(avoid, stream.cuda_stream)
+        if replace:
+            count, size = 0, nbytes
+            if held is not None:
+                count = held.replacements + (held.nbytes >= nbytes)
+                size = max(nbytes, held.nbytes)
+                held.release()
+                del _held[index]
+            held = _Held(torch.device("cuda", index), size, avoid, stream.cuda_stream, count)
+            _held[index] = held
+        launch(held.pointer)
+        held.event = torch.cuda.Event()
+        held.event.record(stream)
+
+
+def held_info() -> dict[int, dict]:
+    """Per device: bytes of the held workspace, whether its last placement
+    found another region, and how often it was placed again."""
+    with _lock:
+        return {index: {"bytes": h.nbytes, "other_region": h.moved, "replacements": h.replacements}
+                for index, h in _held.items()}
+
+
+def release_all() -> None:
+    """Free every held workspace (waits for its last use)."""
+    with _lock:
+        for held in _held.values():
+            held.release()
+        _held.clear()
+
+
+__all__ = ["run_with_workspace", "held_info", "release_all", "PLACE_MIN_BYTES"]

@@ -28,6 +28,7 @@ from . import _native
 from .cg import sparse_terms
 from .graph import LunaTPGraph
 from .layout import TensorProductPaths
+from .placement import run_with_workspace
 
 
 def build_uvu_conv_metadata(tp, coefficient_dtype=torch.float32) -> dict:
@@ -297,17 +298,21 @@ def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, T
         size = ctypes.c_size_t()
         _native.check(lib.luna_uvu_conv_bwd_workspace(plan.handle, N, E, ctypes.byref(size)),
                       "luna_uvu_conv_bwd_workspace")
-        workspace = None
+
+        def launch(workspace):
+            _native.check(lib.luna_uvu_conv_bwd(
+                plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w), _native.ptr(env),
+                g.data_ptr(), _native.ptr(gl0) if (gl0 is not None and gl0.numel()) else None,
+                graph.src.data_ptr(), graph.dst_rowptr.data_ptr(), graph.node_order.data_ptr(),
+                graph.src_rowptr.data_ptr(), graph.edge_ids_by_src.data_ptr(),
+                _native.ptr(gx), _native.ptr(gy), _native.ptr(gw), _native.ptr(genv),
+                workspace, size.value if workspace is not None else 0,
+                N, E, _stream(x)), "luna_uvu_conv_bwd")
+
         if (need_x or need_y or need_env) and E:
-            workspace = torch.empty(size.value, device=x.device, dtype=torch.uint8)
-        _native.check(lib.luna_uvu_conv_bwd(
-            plan.handle, x.data_ptr(), _native.ptr(y), _native.ptr(w), _native.ptr(env),
-            g.data_ptr(), _native.ptr(gl0) if (gl0 is not None and gl0.numel()) else None,
-            graph.src.data_ptr(), graph.dst_rowptr.data_ptr(), graph.node_order.data_ptr(),
-            graph.src_rowptr.data_ptr(), graph.edge_ids_by_src.data_ptr(),
-            _native.ptr(gx), _native.ptr(gy), _native.ptr(gw), _native.ptr(genv),
-            _native.ptr(workspace), size.value if workspace is not None else 0,
-            N, E, _stream(x)), "luna_uvu_conv_bwd")
+            run_with_workspace(x.device, size.value, gw if gw is not None else gx, launch)
+        else:
+            launch(None)
     if gy is not None and not E:
         gy.zero_()
     return gx, gy, gw, genv

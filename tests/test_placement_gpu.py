@@ -1,0 +1,91 @@
+"""Region-placed backward workspaces: the probe, the held buffer, and that
+the backward's outputs do not depend on where its workspace lies."""
+
+import ctypes
+
+import pytest
+import torch
+
+import lunaequivariance_amd as lunaeq
+from lunaequivariance_amd import _native, placement
+from tests.conftest import mace_irreps
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+MB = 1 << 20
+
+
+@pytest.fixture
+def small_placement(monkeypatch):
+    """Place workspaces from 256 MB on, with at most 4 GB of spacers."""
+    placement.release_all()
+    monkeypatch.setattr(placement, "PLACE_MIN_BYTES", 256 * MB)
+    monkeypatch.setenv("LUNAEQ_AMD_PLACE", "1")
+    monkeypatch.setenv("LUNAEQ_AMD_PLACE_SPACER_GB", "4")
+    yield
+    placement.release_all()
+
+
+def test_probe_finds_two_parts_of_one_buffer_in_one_region():
+    a = torch.empty(1024 * MB, dtype=torch.uint8, device=DEV)
+    same = ctypes.c_int(-1)
+    stream = torch.cuda.current_stream().cuda_stream
+    _native.check(_native.lib().luna_same_region(a.data_ptr(), 768 * MB, a.data_ptr() + 768 * MB, 256 * MB,
+                                                 stream, ctypes.byref(same)), "luna_same_region")
+    assert same.value == 1
+
+
+def test_probe_and_placement_reject_small_buffers():
+    a = torch.empty(300 * MB, dtype=torch.uint8, device=DEV)
+    same = ctypes.c_int()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert _native.lib().luna_same_region(a.data_ptr(), 300 * MB, a.data_ptr(), 300 * MB, stream,
+                                          ctypes.byref(same)) != 0
+    assert b"512 MB" in _native.lib().luna_last_error()
+    out, moved = ctypes.c_void_p(), ctypes.c_int()
+    assert _native.lib().luna_placed_alloc(64 * MB, None, 0, 1 << 30, stream, ctypes.byref(out),
+                                           ctypes.byref(moved)) != 0
+    assert out.value is None
+
+
+def test_held_workspace_is_reused_and_grows(small_placement):
+    seen = []
+    grad = torch.empty(600 * MB, dtype=torch.uint8, device=DEV)
+    placement.run_with_workspace(torch.device(DEV), 300 * MB, grad, seen.append)
+    placement.run_with_workspace(torch.device(DEV), 280 * MB, grad, seen.append)
+    assert seen[0] == seen[1] and seen[0] is not None
+    info = placement.held_info()[torch.cuda.current_device()]
+    assert info["bytes"] == 300 * MB and info["replacements"] == 0
+    placement.run_with_workspace(torch.device(DEV), 400 * MB, grad, seen.append)
+    assert placement.held_info()[torch.cuda.current_device()]["bytes"] == 400 * MB
+    # Below the threshold: an ordinary allocation, nothing held changes.
+    placement.run_with_workspace(torch.device(DEV), 8 * MB, grad, seen.append)
+    assert placement.held_info()[torch.cuda.current_device()]["bytes"] == 400 * MB
+
+
+def test_backward_outputs_do_not_depend_on_the_workspace(small_placement, monkeypatch):
+    """The same backward with a placed and with an ordinary workspace (bitwise:
+    the kernels' summation order does not depend on where the workspace is)."""
+    in1, sh, out, instructions = mace_irreps(128, 3)
+    conv = lunaeq.TensorProductConv(in1, sh, out, instructions, internal_weights=False,
+                                    shared_weights=False, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(11)
+    nodes, edges = 1000, 40000  # workspace: 40000 edges x 8 KB of messages + gy partials > 256 MB
+    src = torch.randint(nodes, (edges,), generator=gen)
+    dst = torch.sort(torch.randint(nodes, (edges,), generator=gen))[0]
+    graph = conv.create_graph(src.to(DEV), dst.to(DEV), nodes)
+    x = torch.randn(nodes, conv.irreps_in1.dim, generator=gen).to(DEV).requires_grad_()
+    y = torch.randn(edges, conv.irreps_in2.dim, generator=gen).to(DEV).requires_grad_()
+    w = torch.randn(edges, conv.weight_numel, generator=gen).to(DEV).requires_grad_()
+    g = torch.randn(nodes, conv.irreps_out.dim, generator=gen).to(DEV)
+
+    def grads():
+        return torch.autograd.grad(conv(x, y, w, graph=graph), (x, y, w), g)
+
+    placed = grads()
+    assert placement.held_info(), "the workspace was not placed"
+    monkeypatch.setenv("LUNAEQ_AMD_PLACE", "0")
+    plain = grads()
+    for a, b, name in zip(placed, plain, ("gx", "gy", "gw")):
+        assert torch.equal(a, b), name
