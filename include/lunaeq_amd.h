@@ -136,28 +136,34 @@ int luna_uvu_conv_bwd(const LunaUvuPlan* plan,
                       int64_t num_nodes, int64_t num_edges, LunaStream stream);
 
 /*
- * Device buffer of `bytes` (at least 256 MB) placed outside the HBM region of
- * `avoid` (a device buffer of avoid_bytes >= 512 MB whose contents the probe
+ * Device buffer of `bytes` (at least 1 GB) placed outside the HBM region of
+ * `avoid` (a device buffer of avoid_bytes >= 2 GB whose contents the probe
  * overwrites; NULL: outside the region the allocator is filling now).
  * Concurrent writes to two buffers run about 25 % faster when the buffers lie
  * in different ~96 GB regions of the device than in one; the backward's
  * message workspace is placed this way against the weight gradient it is
- * written beside.  The region of a fresh allocation is found by measurement
- * (luna_same_region); allocations that land in the avoided region are held as
- * spacers, up to max_spacer_bytes and while free memory allows, and released
- * on return.  *moved is 1 when the buffer lies in another region, 0 when the
- * search gave up or max_spacer_bytes is 0 (the buffer is then an ordinary
- * allocation, and with 0 nothing is probed).  Synchronises `stream`.  Release
- * with luna_placed_free.  No counterpart in the reference.
+ * written beside.  The regions of a fresh allocation are found by measurement
+ * (as in luna_region_overlap); allocations whose overlap with `avoid` exceeds
+ * 0.25 are held as spacers, up to max_spacer_bytes and while free memory
+ * allows, and released on return.  *moved is 1 when the returned buffer's
+ * overlap is at most 0.25, 0 when the search gave up (the least overlapping
+ * candidate is returned) or max_spacer_bytes is 0 (an ordinary allocation,
+ * nothing probed).  Synchronises `stream`.  Release with luna_placed_free.
+ * No counterpart in the reference.
  */
 int luna_placed_alloc(size_t bytes, void* avoid, size_t avoid_bytes, size_t max_spacer_bytes,
                       LunaStream stream, void** out, int* moved);
 /*
- * *same = 1 when b lies in the HBM region of a (writing 256 MB of a and of b
- * together is not faster than writing two 256 MB parts of a together).
- * Overwrites the first 512 MB of a and 256 MB of b; synchronises `stream`.
+ * *overlap = expected share of write pairs that meet in one HBM region when
+ * a and b are written together: fa fb + (1 - fa)(1 - fb), where fa and fb are
+ * the shares of up to four 1 GB windows of each buffer (start, thirds, end)
+ * found in the region of a's first window by a write probe.  1 for two parts
+ * of one region, 0 for buffers in different regions.  a_bytes >= 2 GB,
+ * b_bytes >= 1 GB.  Overwrites the first 2 GB of a and the windows of a and
+ * b; synchronises `stream`.
  */
-int luna_same_region(void* a, size_t a_bytes, void* b, size_t b_bytes, LunaStream stream, int* same);
+int luna_region_overlap(void* a, size_t a_bytes, void* b, size_t b_bytes, LunaStream stream,
+                        double* overlap);
 int luna_placed_free(void* pointer);
 
 /*

@@ -56,8 +56,8 @@ PROTOTYPES = {
                           + [ctypes.c_size_t, _I64, _I64, _VP]),
     "luna_placed_alloc": (ctypes.c_int, [ctypes.c_size_t, _VP, ctypes.c_size_t, ctypes.c_size_t, _VP,
                                           ctypes.POINTER(_VP), ctypes.POINTER(ctypes.c_int)]),
-    "luna_same_region": (ctypes.c_int, [_VP, ctypes.c_size_t, _VP, ctypes.c_size_t, _VP,
-                                         ctypes.POINTER(ctypes.c_int)]),
+    "luna_region_overlap": (ctypes.c_int, [_VP, ctypes.c_size_t, _VP, ctypes.c_size_t, _VP,
+                                            ctypes.POINTER(ctypes.c_double)]),
     "luna_placed_free": (ctypes.c_int, [_VP]),
     "luna_graph_bounds": (ctypes.c_int, [_VP, _VP, ctypes.c_int, _I64, _VP, _VP]),
     "luna_graph_workspace": (ctypes.c_int, [_I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),

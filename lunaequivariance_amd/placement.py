@@ -5,14 +5,16 @@ The convolution backwards write the weight gradient and their per-edge gx
 messages at the same time.  Device memory on MI355X falls into regions of
 about 96 GB, and two buffers written together move about 25 % more bytes per
 second when they lie in different regions (config-2 backward 9.7 -> 8.7 ms
-with the message workspace away from the gradient; a 2 x 256 MB write probe
-tells the two cases apart).  A workspace of at least ``PLACE_MIN_BYTES`` is
+with the message workspace away from the gradient; 1 GB write probes at
+up to four windows of each buffer tell the cases apart, since a buffer of
+several GB may straddle two regions).  A workspace of at least ``PLACE_MIN_BYTES`` is
 therefore held per device: ``luna_placed_alloc`` allocates it outside the
 region of the gradient buffer of the call that needs it, and every later
 call that fits in it reuses it.  A later call whose gradient buffer is new
-probes it once against the held workspace (``luna_same_region``; the probe
-overwrites part of the gradient buffer before the kernels fill it) and, if
-they share a region, places the workspace again, at most
+probes it once against the held workspace (``luna_region_overlap``; the
+probe overwrites parts of the gradient buffer before the kernels fill it)
+and, if more than half of their write pairs would meet in one region, places
+the workspace again, at most
 ``MAX_REPLACEMENTS`` times per device.  Smaller workspaces, calls under HIP
 graph capture and ``LUNAEQ_AMD_PLACE=0`` use an ordinary stream-ordered
 torch allocation.
@@ -33,8 +35,9 @@ import torch
 from . import _native
 
 PLACE_MIN_BYTES = 1 << 30
-PROBE_BYTES = 512 << 20  # what a probe overwrites of the gradient buffer
+PROBE_BYTES = 2 << 30    # least gradient size the probe places against
 MAX_REPLACEMENTS = 3
+SHARED_OVERLAP = 0.5    # re-place when more write pairs than this share a region
 
 
 def _enabled() -> bool:
@@ -63,16 +66,17 @@ class _Held:
         self.device, self.pointer, self.nbytes = device, pointer.value, nbytes
         self.moved = bool(moved.value)
         self.replacements = replacements
-        self.verdicts = {avoid_ptr: not self.moved} if avoid_ptr else {}
+        # Whatever the search found is the best placement for this gradient.
+        self.verdicts = {avoid_ptr: False} if avoid_ptr else {}
         self.event = None
 
     def shares_region(self, avoid, stream: int) -> bool:
         key = avoid.data_ptr()
         if key not in self.verdicts:
-            same = ctypes.c_int()
-            _native.check(_native.lib().luna_same_region(key, _nbytes(avoid), self.pointer, self.nbytes, stream,
-                                                         ctypes.byref(same)), "luna_same_region")
-            self.verdicts[key] = bool(same.value)
+            overlap = ctypes.c_double()
+            _native.check(_native.lib().luna_region_overlap(key, _nbytes(avoid), self.pointer, self.nbytes,
+                                                            stream, ctypes.byref(overlap)), "luna_region_overlap")
+            self.verdicts[key] = overlap.value > SHARED_OVERLAP
         return self.verdicts[key]
 
     def release(self) -> None:
@@ -91,7 +95,7 @@ def run_with_workspace(device: torch.device, nbytes: int, avoid, launch) -> None
     """Call ``launch(pointer)`` with a device workspace of ``nbytes``.
 
     ``avoid`` is the gradient the launch writes beside the workspace (a probe
-    may overwrite its first 512 MB before ``launch`` fills it) or None.
+    may overwrite parts of it before ``launch`` fills it) or None.
     """
     stream = torch.cuda.current_stream(device)
     if not _enabled() or nbytes < PLACE_MIN_BYTES or torch.cuda.is_current_stream_capturing():

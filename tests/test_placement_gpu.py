@@ -18,50 +18,50 @@ MB = 1 << 20
 
 @pytest.fixture
 def small_placement(monkeypatch):
-    """Place workspaces from 256 MB on, with at most 4 GB of spacers."""
+    """Place workspaces from 1 GB on, with at most 8 GB of spacers."""
     placement.release_all()
-    monkeypatch.setattr(placement, "PLACE_MIN_BYTES", 256 * MB)
+    monkeypatch.setattr(placement, "PLACE_MIN_BYTES", 1024 * MB)
     monkeypatch.setenv("LUNAEQ_AMD_PLACE", "1")
-    monkeypatch.setenv("LUNAEQ_AMD_PLACE_SPACER_GB", "4")
+    monkeypatch.setenv("LUNAEQ_AMD_PLACE_SPACER_GB", "8")
     yield
     placement.release_all()
 
 
 def test_probe_finds_two_parts_of_one_buffer_in_one_region():
-    a = torch.empty(1024 * MB, dtype=torch.uint8, device=DEV)
-    same = ctypes.c_int(-1)
+    a = torch.empty(3072 * MB, dtype=torch.uint8, device=DEV)
+    overlap = ctypes.c_double(-1.0)
     stream = torch.cuda.current_stream().cuda_stream
-    _native.check(_native.lib().luna_same_region(a.data_ptr(), 768 * MB, a.data_ptr() + 768 * MB, 256 * MB,
-                                                 stream, ctypes.byref(same)), "luna_same_region")
-    assert same.value == 1
+    _native.check(_native.lib().luna_region_overlap(a.data_ptr(), 2048 * MB, a.data_ptr() + 2048 * MB, 1024 * MB,
+                                                    stream, ctypes.byref(overlap)), "luna_region_overlap")
+    assert overlap.value == 1.0
 
 
 def test_probe_and_placement_reject_small_buffers():
-    a = torch.empty(300 * MB, dtype=torch.uint8, device=DEV)
-    same = ctypes.c_int()
+    a = torch.empty(1500 * MB, dtype=torch.uint8, device=DEV)
+    overlap = ctypes.c_double()
     stream = torch.cuda.current_stream().cuda_stream
-    assert _native.lib().luna_same_region(a.data_ptr(), 300 * MB, a.data_ptr(), 300 * MB, stream,
-                                          ctypes.byref(same)) != 0
-    assert b"512 MB" in _native.lib().luna_last_error()
+    assert _native.lib().luna_region_overlap(a.data_ptr(), 1500 * MB, a.data_ptr(), 1500 * MB, stream,
+                                             ctypes.byref(overlap)) != 0
+    assert b"2 GB" in _native.lib().luna_last_error()
     out, moved = ctypes.c_void_p(), ctypes.c_int()
-    assert _native.lib().luna_placed_alloc(64 * MB, None, 0, 1 << 30, stream, ctypes.byref(out),
+    assert _native.lib().luna_placed_alloc(512 * MB, None, 0, 1 << 30, stream, ctypes.byref(out),
                                            ctypes.byref(moved)) != 0
     assert out.value is None
 
 
 def test_held_workspace_is_reused_and_grows(small_placement):
     seen = []
-    grad = torch.empty(600 * MB, dtype=torch.uint8, device=DEV)
-    placement.run_with_workspace(torch.device(DEV), 300 * MB, grad, seen.append)
-    placement.run_with_workspace(torch.device(DEV), 280 * MB, grad, seen.append)
+    grad = torch.empty(2500 * MB, dtype=torch.uint8, device=DEV)
+    placement.run_with_workspace(torch.device(DEV), 1100 * MB, grad, seen.append)
+    placement.run_with_workspace(torch.device(DEV), 1050 * MB, grad, seen.append)
     assert seen[0] == seen[1] and seen[0] is not None
     info = placement.held_info()[torch.cuda.current_device()]
-    assert info["bytes"] == 300 * MB and info["replacements"] == 0
-    placement.run_with_workspace(torch.device(DEV), 400 * MB, grad, seen.append)
-    assert placement.held_info()[torch.cuda.current_device()]["bytes"] == 400 * MB
+    assert info["bytes"] == 1100 * MB and info["replacements"] == 0
+    placement.run_with_workspace(torch.device(DEV), 1200 * MB, grad, seen.append)
+    assert placement.held_info()[torch.cuda.current_device()]["bytes"] == 1200 * MB
     # Below the threshold: an ordinary allocation, nothing held changes.
     placement.run_with_workspace(torch.device(DEV), 8 * MB, grad, seen.append)
-    assert placement.held_info()[torch.cuda.current_device()]["bytes"] == 400 * MB
+    assert placement.held_info()[torch.cuda.current_device()]["bytes"] == 1200 * MB
 
 
 def test_backward_outputs_do_not_depend_on_the_workspace(small_placement, monkeypatch):
@@ -71,7 +71,7 @@ def test_backward_outputs_do_not_depend_on_the_workspace(small_placement, monkey
     conv = lunaeq.TensorProductConv(in1, sh, out, instructions, internal_weights=False,
                                     shared_weights=False, dtype=torch.float32)
     gen = torch.Generator().manual_seed(11)
-    nodes, edges = 1000, 40000  # workspace: 40000 edges x 8 KB of messages + gy partials > 256 MB
+    nodes, edges = 3000, 140000  # workspace: 140000 edges x 8 KB of messages + gy partials > 1 GB
     src = torch.randint(nodes, (edges,), generator=gen)
     dst = torch.sort(torch.randint(nodes, (edges,), generator=gen))[0]
     graph = conv.create_graph(src.to(DEV), dst.to(DEV), nodes)
