@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "../../include/lunaeq_amd.h"
@@ -81,10 +83,17 @@ struct RegionProbe {
   char* ref;
   hipStream_t stream;
   float same_ms;
+  bool log;
   RegionProbe(void* reference, hipStream_t s) : ref((char*)reference), stream(s) {
+    log = std::getenv("LUNAEQ_AMD_PROBE_LOG") != nullptr;
     same_ms = pair_write_ms(ref, ref + kProbeBytes, stream);
+    if (log) std::fprintf(stderr, "probe ref %p: %.3f ms\n", (void*)ref, same_ms);
   }
-  bool same(void* window) const { return pair_write_ms(ref, window, stream) >= kOtherRegion * same_ms; }
+  bool same(void* window) const {
+    const float ms = pair_write_ms(ref, window, stream);
+    if (log) std::fprintf(stderr, "probe %p: %.3f ms (%s)\n", window, ms, ms >= kOtherRegion * same_ms ? "same" : "other");
+    return ms >= kOtherRegion * same_ms;
+  }
   // Fraction of the sampled windows of [p, p + bytes) in the reference's class.
   double fraction_same(void* p, size_t bytes, bool p_is_ref) const {
     std::vector<size_t> offsets = {0};
