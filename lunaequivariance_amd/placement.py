@@ -16,8 +16,10 @@ probe overwrites parts of the gradient buffer before the kernels fill it)
 and, if more than half of their write pairs would meet in one region, places
 the workspace again, at most
 ``MAX_REPLACEMENTS`` times per device.  Smaller workspaces, calls under HIP
-graph capture and ``LUNAEQ_AMD_PLACE=0`` use an ordinary stream-ordered
-torch allocation.
+graph capture, fp64 backwards and ``LUNAEQ_AMD_PLACE=0`` use an ordinary
+stream-ordered torch allocation.  (fp64, config 3: the backward is bound by
+its FP64 issue and gained nothing, while the relocated workspace tended to
+land beside gx, whose pass then took 3.34-3.38 instead of 2.92 ms.)
 
 The held buffer is ordered across streams by one event per device: a call
 waits for the previous call's work before it writes the buffer, and records
@@ -91,14 +93,16 @@ _lock = threading.Lock()
 _held: dict[int, _Held] = {}
 
 
-def run_with_workspace(device: torch.device, nbytes: int, avoid, launch) -> None:
+def run_with_workspace(device: torch.device, nbytes: int, avoid, launch, place: bool = True) -> None:
     """Call ``launch(pointer)`` with a device workspace of ``nbytes``.
 
     ``avoid`` is the gradient the launch writes beside the workspace (a probe
-    may overwrite parts of it before ``launch`` fills it) or None.
+    may overwrite parts of it before ``launch`` fills it) or None; ``place``
+    False takes an ordinary allocation.
     """
     stream = torch.cuda.current_stream(device)
-    if not _enabled() or nbytes < PLACE_MIN_BYTES or torch.cuda.is_current_stream_capturing():
+    if (not place or not _enabled() or nbytes < PLACE_MIN_BYTES
+            or torch.cuda.is_current_stream_capturing()):
         scratch = torch.empty(nbytes, device=device, dtype=torch.uint8)
         launch(scratch.data_ptr())
         return

@@ -310,7 +310,8 @@ def run_backward(op, x, y, w, graph, g, env=None, gl0=None, needs=(True, True, T
                 N, E, _stream(x)), "luna_uvu_conv_bwd")
 
         if (need_x or need_y or need_env) and E:
-            run_with_workspace(x.device, size.value, gw if gw is not None else gx, launch)
+            run_with_workspace(x.device, size.value, gw if gw is not None else gx, launch,
+                               place=x.dtype == torch.float32)
         else:
             launch(None)
     if gy is not None and not E:
