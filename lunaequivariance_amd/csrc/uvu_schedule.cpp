@@ -227,7 +227,9 @@ void build_schedule(Plan& plan) {
   // the register budget (halved for fp64, whose values take two registers);
   // the backward keeps one group per input block, because split groups would
   // have to accumulate their gx messages.
-  plan.fwd_groups = make_groups(spec, kAccumulatorRegisters / (spec.dtype_bits / 32));
+  int acc_regs = kAccumulatorRegisters;
+  if (const char* e = std::getenv("LUNAEQ_AMD_FACC")) acc_regs = std::max(8, std::atoi(e));
+  plan.fwd_groups = make_groups(spec, acc_regs / (spec.dtype_bits / 32));
   auto out_ranges = [](const Group& g) {
     std::vector<std::pair<long, long>> r;
     for (const auto& b : g.blocks) r.push_back({b.out_off, b.out_off + (long)g.channels * b.d3});
