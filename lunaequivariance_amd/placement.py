@@ -123,7 +123,14 @@ def run_with_workspace(device: torch.device, nbytes: int, avoid, launch, place: 
                 size = max(nbytes, held.nbytes)
                 held.release()
                 del _held[index]
-            held = _Held(torch.device("cuda", index), size, avoid, stream.cuda_stream, count)
+            try:
+                held = _Held(torch.device("cuda", index), size, avoid, stream.cuda_stream, count)
+            except RuntimeError:
+                # No device memory outside torch's cache: an ordinary
+                # allocation (torch may free cached blocks for it).
+                scratch = torch.empty(nbytes, device=device, dtype=torch.uint8)
+                launch(scratch.data_ptr())
+                return
             _held[index] = held
         launch(held.pointer)
         held.event = torch.cuda.Event()
