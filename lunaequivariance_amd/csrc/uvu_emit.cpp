@@ -67,7 +67,9 @@ struct Options {
                          // forward 9.7 -> 8.9 ms, backward unchanged)
   bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
   int lds_reduce = -1;   // gy partials summed over the 64 lanes through LDS (1) or by a
-                         // butterfly of lane exchanges (0); -1: LDS for fp64
+                         // butterfly of lane exchanges (0); -1: LDS (fp64 backward
+                         // 18.7 -> 17.8 ms; fp32 config 2 8.86 -> 8.77 and 9.27 -> 9.17 ms
+                         // in interleaved in-process pairs)
   int hoist_regs = -1;   // registers the backward may spend on q classes computed once
                          // per node instead of per edge (-1: by precision)
   int fwd_local = 0;     // forward in per-path form (no products shared between
@@ -602,7 +604,7 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
   const int bits = spec.dtype_bits;
   GroupUse use = group_use(spec, g);
   const int np = (int)g.paths.size();
-  const bool lds_reduce = opt.lds_reduce < 0 ? bits == 64 : opt.lds_reduce != 0;
+  const bool lds_reduce = opt.lds_reduce != 0;
   if (g.subsets > 1)
     c.line("    const int u = ((slot - %d) / %d) * 64 + lane;", g.slot_base, g.subsets);
   else
@@ -1050,7 +1052,7 @@ std::string emit_backward(const Plan& plan, bool env, bool gl0, bool want_gw, bo
     bool combined = false;
     for (const Group& g : plan.bwd_groups) combined = combined || (g.phase == phase && g.combine_subsets);
     if (combined && want_part) c.line("  __shared__ real gy_sub[2][2][PART_W];");
-    if (want_part && (opt.lds_reduce < 0 ? spec.dtype_bits == 64 : opt.lds_reduce != 0)) {
+    if (want_part && opt.lds_reduce != 0) {
       // Per-wave table of the LDS reduction of the gy partials.
       int most = 1;
       for (const Group& g : plan.bwd_groups)

@@ -382,7 +382,9 @@ void build_schedule(Plan& plan) {
   plan.bwd_phases = bwd_phases;
   plan.bwd_phase_slots = slots;
   // The backward uses the forward's two waves per workgroup.
-  for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(any_split ? 2 : std::min(s, limit));
+  int bwd_limit = limit;
+  if (const char* e = std::getenv("LUNAEQ_AMD_BWG")) bwd_limit = std::max(0, std::min(16, std::atoi(e)));
+  for (int s : plan.bwd_phase_slots) plan.bwd_block_waves.push_back(any_split ? 2 : std::min(s, bwd_limit));
   // A group whose two chunks are the two waves of one workgroup adds their gy
   // partials through LDS and writes one slot (half the partial traffic).
   bool pair = true;
