@@ -61,10 +61,13 @@ struct Options {
   bool nt_w = false;     // the setting of the kernel being emitted
   bool nt_gw = true;     // non-temporal stores of the weight gradient
   int nt_msg = -1;       // non-temporal stores of the gx messages (-1: as bwd_nt_w)
-  int y_vgpr = -1;       // copy y into vector registers before use: a scalar
-                         // operand makes an fp32 VALU op issue at half rate
-                         // (-1: fp32 only; fp64 without the copies measured
-                         // forward 9.7 -> 8.9 ms, backward unchanged)
+  int y_vgpr = -1;       // copy y into vector registers before use (a scalar
+                         // operand makes an fp32 FMA issue 1.45x slower); -1: in
+                         // the fp32 forward only (fp64 without the copies:
+                         // forward 9.7 -> 8.9 ms, backward unchanged; fp32
+                         // backward without them 8.66 -> 8.59 ms, 162 -> 155
+                         // VGPRs, interleaved in-process pairs; fp32 forward
+                         // the same either way)
   bool hoist = false;    // let the backward hoist edge-invariant q_ij out of the edge loop
   int lds_reduce = -1;   // gy partials summed over the 64 lanes through LDS (1) or by a
                          // butterfly of lane exchanges (0); -1: LDS (fp64 backward
@@ -720,7 +723,7 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
     // instead of holding all of them in registers across it.
     for (const auto& name : seeds) c.line("      asm volatile(\"\" : \"+v\"(%s));", name.c_str());
   }
-  YCopies ycopy{opt.y_vgpr < 0 ? spec.dtype_bits == 32 : opt.y_vgpr != 0, {}};
+  YCopies ycopy{opt.y_vgpr > 0, {}};
   for (int i = 0; i < g.d1; ++i) c.line("      real M%d = 0;", i);
   for (int yi : use.ys) c.line("      real GY%d = 0;", yi);
   if (env) c.line("      real GE = 0;");
