@@ -654,7 +654,7 @@ void emit_backward_wave(Code& c, const Spec& spec, const Group& g, bool env, boo
       }
     }
     const int per_value = bits / 32;
-    int budget = opt.hoist_regs >= 0 ? opt.hoist_regs : (bits == 32 ? 24 : 36);
+    int budget = opt.hoist_regs >= 0 ? opt.hoist_regs : 36;
     std::map<std::string, int> left = users;  // classes per seed not yet hoisted
     int extra = 0;                            // registers: hoisted values minus freed seeds
     auto cost = [&](const Candidate& cd) {
