@@ -89,3 +89,40 @@ def test_backward_outputs_do_not_depend_on_the_workspace(small_placement, monkey
     plain = grads()
     for a, b, name in zip(placed, plain, ("gx", "gy", "gw")):
         assert torch.equal(a, b), name
+
+
+def test_capture_takes_a_torch_workspace(small_placement):
+    """Under HIP graph capture the backward takes a stream-ordered torch
+    workspace (no device allocation in the capture), also while a placed one
+    is held; replays match eager."""
+    in1, sh, out, instructions = mace_irreps(128, 3)
+    conv = lunaeq.TensorProductConv(in1, sh, out, instructions, internal_weights=False,
+                                    shared_weights=False, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(12)
+    nodes, edges = 3000, 140000
+    src = torch.randint(nodes, (edges,), generator=gen)
+    dst = torch.sort(torch.randint(nodes, (edges,), generator=gen))[0]
+    graph = conv.create_graph(src.to(DEV), dst.to(DEV), nodes)
+    sx = torch.randn(nodes, conv.irreps_in1.dim, generator=gen).to(DEV).requires_grad_()
+    sy = torch.randn(edges, conv.irreps_in2.dim, generator=gen).to(DEV).requires_grad_()
+    sw = torch.randn(edges, conv.weight_numel, generator=gen).to(DEV).requires_grad_()
+    sg = torch.randn(nodes, conv.irreps_out.dim, generator=gen).to(DEV)
+
+    def step():
+        return torch.autograd.grad(conv(sx, sy, sw, graph=graph), (sx, sy, sw), sg)
+
+    eager = step()
+    assert placement.held_info(), "the eager call did not place its workspace"
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    captured = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(captured):
+        static = step()
+    for _ in range(2):
+        captured.replay()
+        torch.cuda.synchronize()
+        for a, b, name in zip(static, eager, ("gx", "gy", "gw")):
+            assert torch.equal(a, b), name
