@@ -1,0 +1,148 @@
+"""Host logic of the placed backward workspace (no GPU): when a workspace is
+held, reused, grown or placed again, and when torch allocates instead.  The
+C-ABI calls and torch's device API are replaced by recording fakes."""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from lunaequivariance_amd import placement
+
+GB = 1 << 30
+
+
+class FakeLib:
+    def __init__(self, overlap=0.0, fail_alloc=False):
+        self.overlap = overlap
+        self.fail_alloc = fail_alloc
+        self.allocs, self.frees, self.probes = [], [], 0
+        self.next = 0x1000
+
+    def luna_placed_alloc(self, nbytes, avoid, avoid_bytes, spacer, stream, pointer, moved):
+        if self.fail_alloc:
+            return 1
+        self.next += 0x1000
+        pointer._obj.value = self.next
+        moved._obj.value = 1
+        self.allocs.append((nbytes, avoid))
+        return 0
+
+    def luna_region_overlap(self, a, a_bytes, b, b_bytes, stream, result):
+        self.probes += 1
+        result._obj.value = self.overlap
+        return 0
+
+    def luna_placed_free(self, pointer):
+        self.frees.append(pointer)
+        return 0
+
+    def luna_last_error(self):
+        return b"fake failure"
+
+
+class FakeEvent:
+    def record(self, stream):
+        pass
+
+    def synchronize(self):
+        pass
+
+
+class FakeTensor:
+    """Stands for a device gradient buffer: address and size only."""
+
+    def __init__(self, ptr, nbytes):
+        self.ptr, self.nbytes = ptr, nbytes
+
+    def data_ptr(self):
+        return self.ptr
+
+    def numel(self):
+        return self.nbytes
+
+    def element_size(self):
+        return 1
+
+    def is_contiguous(self):
+        return True
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    lib = FakeLib()
+    stream = SimpleNamespace(cuda_stream=7, wait_event=lambda event: None)
+    capturing = {"on": False}
+    fake_cuda = SimpleNamespace(
+        current_stream=lambda device=None: stream,
+        is_current_stream_capturing=lambda: capturing["on"],
+        current_device=lambda: 0,
+        Event=FakeEvent,
+        device=lambda d: __import__("contextlib").nullcontext(),
+    )
+    fake_torch = SimpleNamespace(cuda=fake_cuda, device=torch.device, uint8=torch.uint8,
+                                 empty=lambda n, device=None, dtype=None: torch.empty(n, dtype=dtype))
+    monkeypatch.setattr(placement, "torch", fake_torch)
+    monkeypatch.setattr(placement._native, "lib", lambda: lib)
+    monkeypatch.setenv("LUNAEQ_AMD_PLACE", "1")
+    placement._held.clear()
+    yield lib, capturing
+    placement._held.clear()
+
+
+def run(nbytes, avoid, place=True):
+    seen = []
+    placement.run_with_workspace(torch.device("cuda", 0), nbytes, avoid, seen.append, place=place)
+    return seen[0]
+
+
+def test_held_buffer_is_reused_grown_and_placed_against_the_gradient(fake):
+    lib, _ = fake
+    grad = FakeTensor(0xA0000, 4 * GB)
+    first = run(2 * GB, grad)
+    assert lib.allocs == [(2 * GB, 0xA0000)]
+    assert run(int(1.5 * GB), grad) == first and lib.probes == 0  # same gradient: no probe
+    run(3 * GB, grad)  # grows: the old buffer is freed, the new one placed
+    assert lib.frees == [first] and len(lib.allocs) == 2
+    assert placement.held_info()[0]["bytes"] == 3 * GB and placement.held_info()[0]["replacements"] == 0
+
+
+def test_new_gradient_is_probed_once_and_replacements_are_bounded(fake):
+    lib, _ = fake
+    run(2 * GB, FakeTensor(0xA0000, 4 * GB))
+    lib.overlap = 0.1
+    run(2 * GB, FakeTensor(0xB0000, 4 * GB))
+    run(2 * GB, FakeTensor(0xB0000, 4 * GB))
+    assert lib.probes == 1 and len(lib.allocs) == 1  # low overlap: kept, verdict cached
+    lib.overlap = 0.9
+    for n in range(placement.MAX_REPLACEMENTS + 2):
+        run(2 * GB, FakeTensor(0xC0000 + n, 4 * GB))
+    assert len(lib.allocs) == 1 + placement.MAX_REPLACEMENTS
+    assert placement.held_info()[0]["replacements"] == placement.MAX_REPLACEMENTS
+
+
+def test_torch_allocates_when_placement_does_not_apply(fake, monkeypatch):
+    lib, capturing = fake
+    grad = FakeTensor(0xA0000, 4 * GB)
+    run(placement.PLACE_MIN_BYTES - 1, grad)  # small
+    run(2 * GB, grad, place=False)  # caller opts out (fp64)
+    capturing["on"] = True
+    run(2 * GB, grad)  # under capture
+    capturing["on"] = False
+    monkeypatch.setenv("LUNAEQ_AMD_PLACE", "0")
+    run(2 * GB, grad)
+    assert lib.allocs == [] and placement.held_info() == {}
+
+
+def test_small_or_absent_gradient_places_against_a_fresh_reference(fake):
+    lib, _ = fake
+    run(2 * GB, FakeTensor(0xA0000, GB))  # below the probe's 2 GB: no buffer to avoid
+    run(2 * GB, None)
+    assert lib.allocs[0] == (2 * GB, None) and lib.probes == 0
+
+
+def test_failed_placement_falls_back_to_torch(fake):
+    lib, _ = fake
+    lib.fail_alloc = True
+    run(2 * GB, FakeTensor(0xA0000, 4 * GB))
+    assert placement.held_info() == {}
